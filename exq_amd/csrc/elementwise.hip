@@ -1,0 +1,171 @@
+// elementwise.hip -- row gather, deterministic combine, SiLU-and-mul, and the
+// library's status plumbing.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "exq_internal.h"
+
+namespace exq {
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+int set_error(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(EXQ_ERROR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return EXQ_SUCCESS;
+}
+
+namespace {
+
+// ---- gather ------------------------------------------------------------------
+// One work-group per sorted row; 16-byte vector copies (row bytes % 16 == 0).
+__global__ void __launch_bounds__(256) gather_rows_kernel(const uint4* __restrict__ hidden,
+                                                          const int64_t* __restrict__ order,
+                                                          uint4* __restrict__ out, int top_k,
+                                                          int vec_per_row, int n_tokens) {
+  const int i = blockIdx.x;
+  const int64_t tok = order[i] / top_k;
+  if (tok < 0 || tok >= n_tokens) return;
+  const uint4* src = hidden + tok * vec_per_row;
+  uint4* dst = out + (int64_t)i * vec_per_row;
+  for (int v = threadIdx.x; v < vec_per_row; v += blockDim.x) dst[v] = src[v];
+}
+
+// ---- combine -----------------------------------------------------------------
+__global__ void inverse_perm_kernel(const int64_t* __restrict__ order, int n,
+                                    int32_t* __restrict__ inv) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const int64_t s = order[i];
+    if (s >= 0 && s < n) inv[s] = i;
+  }
+}
+
+// result[t, h] = sum_j w[t, j] * down[inv[t*k + j], h], j ascending, fp32.
+__global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ down, int dtype,
+                                                      const int32_t* __restrict__ inv,
+                                                      const void* __restrict__ w, int wdtype,
+                                                      int top_k, int H, void* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  if (h >= H) return;
+  float acc = 0.f;
+  for (int j = 0; j < top_k; ++j) {
+    const int64_t slot = (int64_t)t * top_k + j;
+    const int i = inv[slot];
+    acc += load_as_f32(w, wdtype, slot) * load_as_f32(down, dtype, (int64_t)i * H + h);
+  }
+  store_from_f32(out, dtype, (int64_t)t * H + h, acc);
+}
+
+// ---- SiLU-and-mul ------------------------------------------------------------
+__global__ void __launch_bounds__(256) silu_mul_kernel(const void* __restrict__ x, int dtype,
+                                                       int64_t rows, int64_t I,
+                                                       void* __restrict__ out) {
+  const int64_t n = rows * I;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < n;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = idx / I, j = idx - m * I;
+    const float g = load_as_f32(x, dtype, m * 2 * I + j);
+    const float u = load_as_f32(x, dtype, m * 2 * I + I + j);
+    store_from_f32(out, dtype, idx, silu_f32(g) * u);
+  }
+}
+
+}  // namespace
+}  // namespace exq
+
+using namespace exq;
+
+extern "C" int exq_abi_version(void) { return EXQ_ABI_VERSION; }
+
+extern "C" const char* exq_last_error(void) { return g_last_error; }
+
+extern "C" const char* exq_status_name(int status) {
+  switch (status) {
+    case EXQ_SUCCESS: return "EXQ_SUCCESS";
+    case EXQ_ERROR_INVALID_ARGUMENT: return "EXQ_ERROR_INVALID_ARGUMENT";
+    case EXQ_ERROR_UNSUPPORTED: return "EXQ_ERROR_UNSUPPORTED";
+    case EXQ_ERROR_WORKSPACE_TOO_SMALL: return "EXQ_ERROR_WORKSPACE_TOO_SMALL";
+    case EXQ_ERROR_HIP: return "EXQ_ERROR_HIP";
+    default: return "EXQ_ERROR_UNKNOWN";
+  }
+}
+
+extern "C" int exq_gather_hidden(const void* hidden, int dtype, int64_t n_tokens,
+                                 int64_t hidden_size, const int64_t* sort_order,
+                                 int64_t n_active, int64_t top_k, void* out,
+                                 exq_stream stream) {
+  EXQ_REQUIRE(is_float_dtype(dtype), "exq_gather_hidden: dtype must be f32, f16 or bf16");
+  EXQ_REQUIRE(top_k >= 1 && n_active >= 0 && n_active <= INT32_MAX && n_tokens >= 0,
+              "exq_gather_hidden: bad sizes");
+  const int64_t row_bytes = hidden_size * dtype_bytes(dtype);
+  EXQ_REQUIRE(hidden_size > 0 && row_bytes % 16 == 0,
+              "exq_gather_hidden: row bytes (%lld) must be a multiple of 16",
+              (long long)row_bytes);
+  if (n_active == 0) return EXQ_SUCCESS;
+  EXQ_REQUIRE(hidden && sort_order && out, "exq_gather_hidden: null pointer");
+  EXQ_REQUIRE(((uintptr_t)hidden | (uintptr_t)out) % 16 == 0,
+              "exq_gather_hidden: hidden/out must be 16-byte aligned");
+  const int vec = (int)(row_bytes / 16);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((unsigned)n_active), dim3(vec < 256 ? vec : 256),
+                     0, as_stream(stream), reinterpret_cast<const uint4*>(hidden), sort_order,
+                     reinterpret_cast<uint4*>(out), (int)top_k, vec, (int)n_tokens);
+  return check_launch("gather_rows_kernel");
+}
+
+extern "C" size_t exq_combine_workspace_size(int64_t n_active) {
+  return align_up((size_t)(n_active > 0 ? n_active : 0) * sizeof(int32_t), 256);
+}
+
+extern "C" int exq_combine(const void* down_out, int dtype, const int64_t* sort_order,
+                           int64_t n_active, const void* router_weights, int weights_dtype,
+                           int64_t n_tokens, int64_t top_k, int64_t hidden_size, void* result,
+                           void* workspace, size_t workspace_bytes, exq_stream stream) {
+  EXQ_REQUIRE(is_float_dtype(dtype) && is_float_dtype(weights_dtype),
+              "exq_combine: dtypes must be f32, f16 or bf16");
+  EXQ_REQUIRE(top_k >= 1 && n_tokens >= 0 && n_active == n_tokens * top_k &&
+                  n_active <= INT32_MAX && hidden_size > 0,
+              "exq_combine: n_active (%lld) must equal n_tokens*top_k (%lld)",
+              (long long)n_active, (long long)(n_tokens * top_k));
+  if (n_tokens == 0) return EXQ_SUCCESS;
+  if (workspace_bytes < exq_combine_workspace_size(n_active))
+    return set_error(EXQ_ERROR_WORKSPACE_TOO_SMALL, "exq_combine: workspace %zu < %zu bytes",
+                     workspace_bytes, exq_combine_workspace_size(n_active));
+  EXQ_REQUIRE(down_out && sort_order && router_weights && result && workspace,
+              "exq_combine: null pointer");
+  int32_t* inv = reinterpret_cast<int32_t*>(workspace);
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(inverse_perm_kernel, dim3((unsigned)cdiv(n_active, 256)), dim3(256), 0, s,
+                     sort_order, (int)n_active, inv);
+  int st = check_launch("inverse_perm_kernel");
+  if (st) return st;
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)cdiv(hidden_size, 256), (unsigned)n_tokens),
+                     dim3(256), 0, s, down_out, dtype, inv, router_weights, weights_dtype,
+                     (int)top_k, (int)hidden_size, result);
+  return check_launch("combine_kernel");
+}
+
+extern "C" int exq_silu_and_mul(const void* input, int dtype, int64_t rows, int64_t inter,
+                                void* out, exq_stream stream) {
+  EXQ_REQUIRE(is_float_dtype(dtype), "exq_silu_and_mul: dtype must be f32, f16 or bf16");
+  EXQ_REQUIRE(rows >= 0 && inter >= 1, "exq_silu_and_mul: bad sizes");
+  if (rows == 0) return EXQ_SUCCESS;
+  EXQ_REQUIRE(input && out, "exq_silu_and_mul: null pointer");
+  int64_t blocks = cdiv(rows * inter, 256);
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                     input, dtype, rows, inter, out);
+  return check_launch("silu_mul_kernel");
+}

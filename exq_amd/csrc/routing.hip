@@ -1,0 +1,375 @@
+// routing.hip -- routing preparation on one work-group per call.
+//
+// Decode batches route at most a few thousand slots, so a single 1024-thread
+// work-group does the whole job out of LDS: an LDS-atomic histogram, a
+// wave-shuffle block scan, and a stable scatter whose rank comes from
+// per-bucket slot bitmasks (popcount of the lower bits), so the order inside
+// a bucket is deterministic and ascending -- the canonical order of the
+// reference's stable argsort (exq/kernels/moe_grouped_gemm.py:156-157).
+// Nothing here uses global atomics, hipCUB or temporary allocations.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "exq_internal.h"
+
+namespace exq {
+namespace {
+
+constexpr int RT = 1024;            // threads of the routing work-group
+constexpr int RT_WAVES = RT / 64;
+constexpr int MAX_BUCKETS = 1024;   // experts (+ shared / shifted bucket)
+constexpr int MASK_WORDS = 16384;   // 64 KiB of chunk bitmasks
+
+struct RouteLds {
+  int cnt[MAX_BUCKETS];
+  int start[MAX_BUCKETS + 1];
+  int run[MAX_BUCKETS];
+  int wsum[RT_WAVES];
+  uint32_t masks[MASK_WORDS];
+};
+
+// Exclusive scan of one value per thread over the work-group.
+__device__ int block_excl_scan(int v, int* wsum, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < RT_WAVES ? wsum[lane] : 0;
+#pragma unroll
+    for (int d = 1; d < RT_WAVES; d <<= 1) {
+      int y = __shfl_up(w, d, 64);
+      if (lane >= d) w += y;
+    }
+    if (lane < RT_WAVES) wsum[lane] = w;
+  }
+  __syncthreads();
+  const int prefix = wave > 0 ? wsum[wave - 1] : 0;
+  *total = wsum[RT_WAVES - 1];
+  __syncthreads();
+  return prefix + x - v;
+}
+
+template <typename KeyFn>
+__device__ void histogram(int n, int nb, KeyFn key, int* cnt) {
+  for (int b = threadIdx.x; b < nb; b += RT) cnt[b] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < n; i += RT) {
+    int b = key(i);
+    if (b >= 0) atomicAdd(&cnt[b], 1);
+  }
+  __syncthreads();
+}
+
+// Stable scatter: element i with bucket b = key(i) >= 0 is emitted at
+// run[b] + (number of earlier elements in bucket b).  run[] advances.
+template <typename KeyFn, typename EmitFn>
+__device__ void stable_scatter(int n, int nb, KeyFn key, int* run, uint32_t* masks,
+                               EmitFn emit) {
+  const int tid = threadIdx.x;
+  int wpb = MASK_WORDS / (nb > 0 ? nb : 1);
+  if (wpb > RT / 32) wpb = RT / 32;
+  const int chunk = wpb * 32;
+  for (int base = 0; base < n; base += chunk) {
+    for (int w = tid; w < nb * wpb; w += RT) masks[w] = 0u;
+    __syncthreads();
+    const int i = base + tid;
+    const int b = (tid < chunk && i < n) ? key(i) : -1;
+    if (b >= 0) atomicOr(&masks[b * wpb + (tid >> 5)], 1u << (tid & 31));
+    __syncthreads();
+    if (b >= 0) {
+      const uint32_t* m = masks + b * wpb;
+      int r = __popc(m[tid >> 5] & ((1u << (tid & 31)) - 1u));
+      for (int w = 0; w < (tid >> 5); ++w) r += __popc(m[w]);
+      emit(i, b, run[b] + r);
+    }
+    __syncthreads();
+    if (tid < nb) {
+      int c = 0;
+      for (int w = 0; w < wpb; ++w) c += __popc(masks[tid * wpb + w]);
+      run[tid] += c;
+    }
+    __syncthreads();
+  }
+}
+
+// ---- exq_dispatch -----------------------------------------------------------
+__global__ void __launch_bounds__(RT) dispatch_kernel(const void* ids, int ids_dtype, int n,
+                                                      int E, int64_t* sort_order,
+                                                      int64_t* sorted_ids, int32_t* ends) {
+  __shared__ RouteLds s;
+  // Ids outside [0, E) go to a trailing bucket E so sort_order stays a permutation.
+  auto key = [&](int i) -> int {
+    int64_t v = load_index(ids, ids_dtype, i);
+    return (v >= 0 && v < E) ? (int)v : E;
+  };
+  const int nb = E + 1;  // <= RT, so one scan pass covers every bucket
+  histogram(n, nb, key, s.cnt);
+  const int b = threadIdx.x;
+  int t;
+  int ex = block_excl_scan(b < nb ? s.cnt[b] : 0, s.wsum, &t);
+  if (b < nb) {
+    s.start[b] = ex;
+    s.run[b] = ex;
+  }
+  if (threadIdx.x == 0) s.start[nb] = t;
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += RT) ends[e] = s.start[e];
+  stable_scatter(n, nb, key, s.run, s.masks, [&](int i, int b, int pos) {
+    sort_order[pos] = i;
+    sorted_ids[pos] = load_index(ids, ids_dtype, i);
+  });
+}
+
+// ---- exq_build_ends_from_slots ---------------------------------------------
+__global__ void __launch_bounds__(RT) build_ends_kernel(const int32_t* sid, int em,
+                                                        const int32_t* fr, int n_active, int E,
+                                                        int32_t* ends, int64_t* sort_order) {
+  __shared__ RouteLds s;
+  auto key = [&](int i) -> int {
+    int slot = sid[i];
+    if (slot < 0 || slot >= n_active) return -1;
+    int e = fr[slot];
+    return (e >= 0 && e < E) ? e : -1;
+  };
+  histogram(em, E, key, s.cnt);
+  int b = threadIdx.x;
+  int t;
+  int ex = block_excl_scan(b < E ? s.cnt[b] : 0, s.wsum, &t);
+  if (b < E) {
+    s.start[b] = ex;
+    s.run[b] = ex;
+  }
+  if (threadIdx.x == 0) s.start[E] = t;
+  __syncthreads();
+  for (int e = threadIdx.x; e <= E; e += RT) ends[e] = s.start[e];
+  stable_scatter(em, E, key, s.run, s.masks,
+                 [&](int i, int, int pos) { sort_order[pos] = sid[i]; });
+}
+
+// ---- exq_moe_align_block_size ----------------------------------------------
+__global__ void __launch_bounds__(RT) align_kernel(const void* ids, int ids_dtype, int numel,
+                                                   int nb, int B, int32_t* sorted_ids, int cap,
+                                                   int32_t* expert_ids, int cap_blocks,
+                                                   int32_t* ntpp, int32_t* cumsum, int pad) {
+  __shared__ RouteLds s;
+  auto key = [&](int i) -> int {
+    int64_t v = load_index(ids, ids_dtype, i) + 1;  // bucket 0 holds id == -1
+    return (v >= 0 && v < nb) ? (int)v : -1;
+  };
+  histogram(numel, nb, key, s.cnt);
+  const int b = threadIdx.x;
+  const int padded = b < nb ? ((s.cnt[b] + B - 1) / B) * B : 0;
+  int t;
+  int ex = block_excl_scan(padded, s.wsum, &t);
+  if (b < nb) {
+    s.start[b] = ex;
+    s.run[b] = ex;
+  }
+  if (threadIdx.x == 0) s.start[nb] = t;
+  __syncthreads();
+  for (int i = threadIdx.x; i <= nb; i += RT) cumsum[i] = s.start[i];
+  if (threadIdx.x == 0) ntpp[0] = t;
+  if (pad) {
+    for (int i = threadIdx.x; i < cap; i += RT) sorted_ids[i] = numel;
+  }
+  // Block -> bucket by binary search over the padded starts.
+  for (int blk = threadIdx.x; blk < cap_blocks; blk += RT) {
+    const int p = blk * B;
+    int val = -1;
+    if (p < t) {
+      int lo = 0, hi = nb - 1;
+      while (lo < hi) {  // last bucket with start <= p
+        int mid = (lo + hi + 1) >> 1;
+        if (s.start[mid] <= p) lo = mid; else hi = mid - 1;
+      }
+      val = lo - 1;
+    }
+    expert_ids[blk] = val;
+  }
+  __syncthreads();  // padding fill must land before the scatter overwrites
+  stable_scatter(numel, nb, key, s.run, s.masks,
+                 [&](int i, int, int pos) { sorted_ids[pos] = i; });
+}
+
+// ---- fused-path routing plan -----------------------------------------------
+__global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
+  __shared__ RouteLds s;
+  auto key = [&](int slot) -> int {
+    const int t = slot / p.kp;
+    const int j = slot - t * p.kp;
+    if (j < p.k) {
+      int64_t v = load_index(p.ids, p.ids_dtype, (int64_t)t * p.k + j);
+      return (v >= 0 && v < p.E) ? (int)v : -1;
+    }
+    return p.E + (j - p.k);
+  };
+  const int nb = p.Ep;
+  histogram(p.n, nb, key, s.cnt);
+  const int b = threadIdx.x;
+  int t;
+  int ex = block_excl_scan(b < nb ? s.cnt[b] : 0, s.wsum, &t);
+  if (b < nb) {
+    s.start[b] = ex;
+    s.run[b] = ex;
+  }
+  if (threadIdx.x == 0) s.start[nb] = t;
+  __syncthreads();
+  for (int e = threadIdx.x; e <= nb; e += RT) p.ends[e] = s.start[e];
+  if (p.ends_out) {
+    for (int e = threadIdx.x; e <= p.E; e += RT) p.ends_out[e] = s.start[e];
+  }
+  stable_scatter(p.n, nb, key, s.run, s.masks, [&](int i, int, int pos) {
+    p.sorted[pos] = i;
+    if (p.sort_order_out) p.sort_order_out[pos] = i;
+  });
+
+  // Token groups, heaviest tier first so long work items start early.
+  const int c = b < nb ? s.cnt[b] : 0;
+  const int ng = (c + kTokenGroup - 1) / kTokenGroup;
+  const int my_tier = (b < nb) ? (p.tier ? (int)p.tier[b] : 2) : -1;
+  int base = 0;
+  for (int tr = (p.tier ? 0 : 2); tr <= 2; ++tr) {
+    int tot;
+    int off = block_excl_scan(my_tier == tr ? ng : 0, s.wsum, &tot);
+    if (my_tier == tr) {
+      for (int g = 0; g < ng; ++g) {
+        const int slot = base + off + g;
+        if (slot < p.tg_cap) {
+          TgEntry te;
+          te.e = b;
+          te.pos0 = s.start[b] + g * kTokenGroup;
+          te.cnt = min(kTokenGroup, c - g * kTokenGroup);
+          te.tier = tr;
+          p.tg[slot] = te;
+        }
+      }
+    }
+    base += tot;
+  }
+  if (threadIdx.x == 0) p.hdr[0] = base < p.tg_cap ? base : p.tg_cap;
+  for (int i = threadIdx.x; i < p.n_counters; i += RT) p.counters[i] = 0;
+  if (base == 0 && p.out) {
+    uint32_t* o = reinterpret_cast<uint32_t*>(p.out);
+    for (int64_t i = threadIdx.x; i < p.out_bytes / 4; i += RT) o[i] = 0u;
+  }
+}
+
+// ---- token groups from user boundaries ------------------------------------------
+__global__ void __launch_bounds__(RT) tg_from_ends_kernel(const int32_t* ends, int E,
+                                                          const int32_t* mask, int tier,
+                                                          int* hdr, TgEntry* tg, int tg_cap) {
+  __shared__ int wsum[RT_WAVES];
+  int base = 0;
+  for (int e0 = 0; e0 < E; e0 += RT) {
+    const int e = e0 + (int)threadIdx.x;
+    int lo = 0, c = 0;
+    if (e < E && (!mask || mask[e] != 0)) {
+      lo = ends[e];
+      c = ends[e + 1] - lo;
+      if (c < 0) c = 0;
+    }
+    const int ng = (c + kTokenGroup - 1) / kTokenGroup;
+    int tot;
+    int off = block_excl_scan(ng, wsum, &tot);
+    for (int g = 0; g < ng; ++g) {
+      const int slot = base + off + g;
+      if (slot < tg_cap) {
+        TgEntry te;
+        te.e = e;
+        te.pos0 = lo + g * kTokenGroup;
+        te.cnt = min(kTokenGroup, c - g * kTokenGroup);
+        te.tier = tier;
+        tg[slot] = te;
+      }
+    }
+    base += tot;
+  }
+  if (threadIdx.x == 0) hdr[0] = base < tg_cap ? base : tg_cap;
+}
+
+}  // namespace
+
+int launch_route_plan(const RoutePlanParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(RT), 0, stream, p);
+  return check_launch("route_plan_kernel");
+}
+
+int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, int tier,
+                        int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream) {
+  hipLaunchKernelGGL(tg_from_ends_kernel, dim3(1), dim3(RT), 0, stream, ends, E, expert_mask,
+                     tier, hdr, tg, tg_cap);
+  return check_launch("tg_from_ends_kernel");
+}
+
+}  // namespace exq
+
+using namespace exq;
+
+extern "C" int exq_dispatch(const void* router_indices, int ids_dtype, int64_t n,
+                            int64_t n_experts, int64_t* sort_order, int64_t* sorted_expert_ids,
+                            int32_t* expert_ends, exq_stream stream) {
+  EXQ_REQUIRE(is_index_dtype(ids_dtype), "exq_dispatch: ids dtype must be i32 or i64");
+  EXQ_REQUIRE(n >= 0 && n <= INT32_MAX, "exq_dispatch: n=%lld out of range", (long long)n);
+  EXQ_REQUIRE(n_experts >= 1 && n_experts < MAX_BUCKETS,
+              "exq_dispatch: n_experts=%lld must be in [1, %d)", (long long)n_experts,
+              MAX_BUCKETS);
+  EXQ_REQUIRE(expert_ends && (n == 0 || (router_indices && sort_order && sorted_expert_ids)),
+              "exq_dispatch: null pointer");
+  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(RT), 0, as_stream(stream), router_indices,
+                     ids_dtype, (int)n, (int)n_experts, sort_order, sorted_expert_ids,
+                     expert_ends);
+  return check_launch("dispatch_kernel");
+}
+
+extern "C" int exq_build_ends_from_slots(const int32_t* sorted_slot_ids, int64_t em,
+                                         const int32_t* flat_router, int64_t n_active,
+                                         int64_t n_experts, int32_t* expert_ends,
+                                         int64_t* sort_order, exq_stream stream) {
+  EXQ_REQUIRE(em >= 0 && em <= INT32_MAX && n_active >= 0 && n_active <= INT32_MAX,
+              "exq_build_ends_from_slots: sizes out of range");
+  EXQ_REQUIRE(n_experts >= 1 && n_experts <= MAX_BUCKETS,
+              "exq_build_ends_from_slots: n_experts=%lld must be in [1, %d]",
+              (long long)n_experts, MAX_BUCKETS);
+  EXQ_REQUIRE(expert_ends && (em == 0 || (sorted_slot_ids && flat_router && sort_order)),
+              "exq_build_ends_from_slots: null pointer");
+  hipLaunchKernelGGL(build_ends_kernel, dim3(1), dim3(RT), 0, as_stream(stream),
+                     sorted_slot_ids, (int)em, flat_router, (int)n_active, (int)n_experts,
+                     expert_ends, sort_order);
+  return check_launch("build_ends_kernel");
+}
+
+extern "C" int exq_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
+                                        int64_t num_experts, int64_t block_size,
+                                        int32_t* sorted_token_ids, int64_t sorted_capacity,
+                                        int32_t* expert_ids, int64_t expert_ids_capacity,
+                                        int32_t* num_tokens_post_pad, int32_t* cumsum,
+                                        int pad_sorted_token_ids, exq_stream stream) {
+  EXQ_REQUIRE(is_index_dtype(ids_dtype), "exq_moe_align_block_size: ids dtype must be i32/i64");
+  EXQ_REQUIRE(numel >= 0 && numel <= INT32_MAX, "exq_moe_align_block_size: numel out of range");
+  EXQ_REQUIRE(num_experts >= 1 && num_experts <= MAX_BUCKETS,
+              "exq_moe_align_block_size: num_experts=%lld must be in [1, %d]",
+              (long long)num_experts, MAX_BUCKETS);
+  EXQ_REQUIRE(block_size >= 1 && block_size <= 4096,
+              "exq_moe_align_block_size: block_size=%lld out of range", (long long)block_size);
+  const int64_t need = numel + num_experts * (block_size - 1);
+  EXQ_REQUIRE(sorted_capacity >= need && need <= INT32_MAX,
+              "exq_moe_align_block_size: sorted_token_ids capacity %lld < %lld",
+              (long long)sorted_capacity, (long long)need);
+  EXQ_REQUIRE(expert_ids_capacity >= cdiv(need, block_size),
+              "exq_moe_align_block_size: expert_ids capacity %lld < %lld",
+              (long long)expert_ids_capacity, (long long)cdiv(need, block_size));
+  EXQ_REQUIRE(sorted_token_ids && expert_ids && num_tokens_post_pad && cumsum &&
+                  (numel == 0 || topk_ids),
+              "exq_moe_align_block_size: null pointer");
+  hipLaunchKernelGGL(align_kernel, dim3(1), dim3(RT), 0, as_stream(stream), topk_ids, ids_dtype,
+                     (int)numel, (int)num_experts, (int)block_size, sorted_token_ids,
+                     (int)sorted_capacity, expert_ids, (int)expert_ids_capacity,
+                     num_tokens_post_pad, cumsum, pad_sorted_token_ids ? 1 : 0);
+  return check_launch("align_kernel");
+}

@@ -1,0 +1,187 @@
+"""The fused INT4 MoE layer on the GPU vs the fp32 dequantise-then-matmul
+oracle.  Tolerance: relative L2 error <= 0.5% (the path's stated bound);
+routing outputs bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from exq_amd import synth
+from oracle import quant, routing
+from tests._helpers import assert_close_rel, banner, oracle_int4_layer
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-3
+
+
+def _pack_gpu(E, I, H, seed, device):
+    from exq_amd.kernels import pack_experts_int4
+    w13, w2 = synth.expert_weights_gpu(E, I, H, seed, device)
+    p13, s13 = pack_experts_int4(w13)
+    p2, s2 = pack_experts_int4(w2)
+    del w13, w2
+    return p13, s13, p2, s2
+
+
+def _routing(cfg, T, device, ids_dtype=torch.int64, w_dtype=torch.float32, layer=0):
+    ids, w = synth.routing(cfg, T, layer)
+    return ids, w, torch.from_numpy(ids).to(ids_dtype).to(device), \
+        torch.from_numpy(w).to(w_dtype).to(device)
+
+
+def _hidden(T, H, seed, device, dtype=torch.bfloat16):
+    return torch.from_numpy(synth.hidden_np(T, H, seed)).to(dtype).to(device)
+
+
+def test_pack_on_gpu_bit_exact(device):
+    from exq_amd.kernels import pack_experts_int4
+    banner("pack_experts_int4 on GPU")
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((4, 256, 1024)) * 0.02).astype(np.float16)
+    w[0, 3] = 0
+    w[1, 7, :128] = 0
+    p, s = pack_experts_int4(torch.from_numpy(w).to(device))
+    rp, rs = quant.pack_experts_int4(w)
+    assert np.array_equal(p.cpu().numpy(), rp)
+    assert np.array_equal(s.cpu().numpy(), rs)
+
+
+SMALL = synth.MoeConfig("small", 9, 256, 128, 4, 2, False)
+MID = synth.MoeConfig("mid", 8, 512, 256, 16, 4, True)
+
+
+@pytest.mark.parametrize("cfg,T", [(SMALL, 1), (SMALL, 3), (SMALL, 40), (MID, 16),
+                                   (MID, 100), (MID, 257)])
+def test_fused_small_shapes(cfg, T, device):
+    from exq_amd.kernels import fused_experts
+    banner(f"fused {cfg.name} T={T}")
+    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, 5 + T, device)
+    ids, w, tid, tw = _routing(cfg, T, device)
+    x = _hidden(T, cfg.hidden, 17 + T, device)
+    so = torch.empty(T * cfg.top_k, dtype=torch.int64, device=device)
+    ends = torch.empty(cfg.n_experts + 1, dtype=torch.int32, device=device)
+    out = fused_experts(x, p13, s13, p2, s2, tw, tid, sort_order_out=so, expert_ends_out=ends)
+    torch.cuda.synchronize()
+    r_so, r_ends, _ = routing.sort_tokens_by_expert(ids, cfg.n_experts)
+    assert np.array_equal(so.cpu().numpy(), r_so)
+    assert np.array_equal(ends.cpu().numpy(), r_ends)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, f"{cfg.name} T={T}")
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64])
+def test_fused_qwen3_shape(T, device):
+    from exq_amd.kernels import fused_experts
+    cfg = synth.CONFIGS["qwen3"]
+    banner(f"fused qwen3 T={T}")
+    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, synth.seed_for(cfg), device)
+    ids, w, tid, tw = _routing(cfg, T, device)
+    x = _hidden(T, cfg.hidden, 100 + T, device)
+    out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, f"qwen3 T={T}")
+
+
+def test_fused_olmoe_shape_determinism_and_dtypes(device):
+    from exq_amd.kernels import fused_experts
+    cfg = synth.CONFIGS["olmoe"]
+    T = 16
+    banner("fused olmoe T=16")
+    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, synth.seed_for(cfg), device)
+    ids, w, tid, tw = _routing(cfg, T, device)
+    x = _hidden(T, cfg.hidden, 1, device)
+    out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, "olmoe T=16 bf16")
+    # bitwise repeatable (no atomics in any accumulation order)
+    for _ in range(3):
+        assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid), out)
+    # int32 ids and bf16 routing weights give the same result
+    out2 = fused_experts(x, p13, s13, p2, s2, tw.to(torch.bfloat16), tid.to(torch.int32))
+    ref2 = oracle_int4_layer(x, p13, s13, p2, s2, ids, tw.to(torch.bfloat16).float().cpu().numpy())
+    assert_close_rel(out2, ref2, TOL, "olmoe T=16 i32 ids, bf16 weights")
+    # fp16 activations use the f16 MFMA path
+    xh = x.to(torch.float16)
+    out3 = fused_experts(xh, p13, s13, p2, s2, tw, tid)
+    assert out3.dtype == torch.float16
+    ref3 = oracle_int4_layer(xh, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out3, ref3, TOL, "olmoe T=16 fp16")
+
+
+def test_fused_dropped_ids_and_edges(device):
+    from exq_amd.kernels import fused_experts
+    cfg = MID
+    banner("fused dropped ids / empty")
+    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, 77, device)
+    ids, w, tid, tw = _routing(cfg, 9, device)
+    ids = ids.copy()
+    ids[0, 1] = -1
+    ids[3, :] = -1
+    ids[5, 2] = cfg.n_experts + 3  # out of range is dropped too
+    tid = torch.from_numpy(ids).to(device)
+    x = _hidden(9, cfg.hidden, 3, device)
+    out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, "dropped ids")
+    assert torch.count_nonzero(out[3]) == 0
+    # every id dropped -> zeros; empty batch -> empty output
+    allbad = torch.full_like(tid, -1)
+    z = fused_experts(x, p13, s13, p2, s2, tw, allbad)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(z) == 0
+    e = fused_experts(x[:0], p13, s13, p2, s2, tw[:0], tid[:0])
+    assert e.shape == (0, cfg.hidden)
+
+
+def test_fused_long_contraction_multi_round(device):
+    """Intermediate 14336 (112 k-blocks) exercises several staging rounds."""
+    from exq_amd.kernels import fused_experts
+    cfg = synth.MoeConfig("mixtral_narrow", 4, 1024, 14336, 4, 2, True, zipf=False)
+    banner("fused long K")
+    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, 4000, device)
+    for T in (3, 40):
+        ids, w, tid, tw = _routing(cfg, T, device)
+        x = _hidden(T, cfg.hidden, T, device)
+        out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+        ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+        assert_close_rel(out, ref, TOL, f"long K T={T}")
+
+
+def test_moe_int4_forward_sorted_output(device):
+    from exq_amd.kernels import moe_int4_forward, sort_tokens_by_expert
+    from oracle import moe
+    banner("moe_int4_forward")
+    cfg = MID
+    p13, s13, _, _ = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, 9, device)
+    ids, w, tid, tw = _routing(cfg, 33, device)
+    x = _hidden(33, cfg.hidden, 2, device)
+    out = moe_int4_forward(x, p13, s13, tid, cfg.n_experts)
+    so, sh, ends, max_tok = sort_tokens_by_expert(tid, x, cfg.n_experts)
+    r_so, r_ends, r_max = routing.sort_tokens_by_expert(ids, cfg.n_experts)
+    assert np.array_equal(so.cpu().numpy(), r_so) and max_tok == r_max
+    a = moe.gather_hidden(x.float().cpu().numpy(), r_so, cfg.top_k)
+    wdq = quant.dequant_int4(p13.cpu().numpy(), s13.cpu().numpy())
+    ref = moe.grouped_gemm_sorted(a, wdq, r_ends)
+    assert_close_rel(out, ref, TOL, "moe_int4_forward")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_moe_grouped_gemm_unquantised(dtype, device):
+    from exq_amd.kernels import moe_grouped_gemm
+    from oracle import moe
+    banner(f"moe_grouped_gemm {dtype}")
+    rng = np.random.default_rng(3)
+    E, N, K, T, k = 8, 96, 384, 21, 2
+    W = torch.from_numpy((rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)).to(dtype)
+    ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)])
+    x = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(dtype)
+    mask = torch.ones(E, dtype=torch.int32)
+    mask[2] = 0
+    out = moe_grouped_gemm(x.to(device), W.to(device), torch.from_numpy(ids).to(device), E,
+                           expert_mask=mask.to(device))
+    r_so, r_ends, _ = routing.sort_tokens_by_expert(ids, E)
+    a = moe.gather_hidden(x.float().numpy(), r_so, k)
+    Wm = W.float().numpy().copy()
+    Wm[2] = 0
+    ref = moe.grouped_gemm_sorted(a, Wm, r_ends)
+    assert_close_rel(out, ref, TOL, f"grouped gemm {dtype}")

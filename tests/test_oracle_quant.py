@@ -1,0 +1,114 @@
+"""Pins of the quantisation oracle: hand-derived known answers, the
+reference's own expectations (zero rows, byte counts) and error bounds."""
+import numpy as np
+import pytest
+
+from oracle import quant
+
+
+def _row(vals, K=128):
+    w = np.zeros((1, K), dtype=np.float16)
+    w[0, :len(vals)] = np.asarray(vals, dtype=np.float16)
+    return w
+
+
+def test_pack_known_bytes_plus_minus_one():
+    # max|w| = 1 -> q = +-7 -> nibbles 15 (k=0, low) and 1 (k=1, high) -> 0x1F.
+    packed, scales = quant.pack_int4_weights(_row([1.0, -1.0]))
+    assert packed.shape == (1, 64) and scales.shape == (1, 1)
+    assert packed[0, 0] == 0x1F
+    assert np.all(packed[0, 1:] == 0x88)  # zeros -> nibble 8 in both halves
+    assert scales[0, 0] == np.float16(1.0 / 7.0)
+
+
+def test_pack_round_half_even_known_answers():
+    # absmax 7 -> scale exactly 1.0, so q = round_half_even(w).
+    vals = [7.0, 2.5, 3.5, -2.5, 0.5, -0.5, 1.5, -7.0]
+    packed, scales = quant.pack_int4_weights(_row(vals))
+    assert scales[0, 0] == np.float16(1.0)
+    # q = 7, 2, 4, -2, 0, 0, 2, -7 -> nibbles 15, 10, 12, 6, 8, 8, 10, 1
+    assert list(packed[0, :4]) == [0xAF, 0x6C, 0x88, 0x1A]
+
+
+def test_pack_zero_row_scale_is_fp32_eps():
+    packed, scales = quant.pack_int4_weights(np.zeros((2, 256), np.float16))
+    assert np.all(packed == 0x88)
+    # fp32 eps = 2^-23 rounds to the fp16 subnormal 2 * 2^-24 (bits 0x0002).
+    assert np.all(scales.view(np.uint16) == 0x0002)
+
+
+def test_group_rule_collapse_and_errors():
+    p, s = quant.pack_int4_weights(np.ones((3, 64), np.float16), group_size=128)
+    assert p.shape == (3, 32) and s.shape == (3, 1)
+    with pytest.raises(ValueError):
+        quant.pack_int4_weights(np.ones((1, 127), np.float16))
+    with pytest.raises(ValueError):
+        quant.pack_int4_weights(np.ones((1, 192), np.float16), group_size=128)
+    assert quant.effective_group_size(256, 128) == 128
+
+
+def test_pack_invariants_random():
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((64, 512)) * 0.02).astype(np.float16)
+    packed, scales = quant.pack_int4_weights(w)
+    lo, hi = packed & 0xF, packed >> 4
+    # |q| <= 7 by construction of the scale, so stored nibbles are 1..15.
+    assert lo.min() >= 1 and hi.min() >= 1 and lo.max() <= 15 and hi.max() <= 15
+    deq = quant.dequant_int4(packed, scales)
+    s32 = np.abs(w.astype(np.float32).reshape(64, 4, 128)).max(-1) / np.float32(7)
+    s16 = scales.astype(np.float32)
+    bound = s32 / 2 + 7 * np.abs(s32 - s16) + 1e-7
+    err = np.abs(w.astype(np.float32) - deq).reshape(64, 4, 128).max(-1)
+    assert np.all(err <= bound)
+    # each group's extreme element is reproduced as +-7 * scale
+    g = w.astype(np.float32).reshape(64, 4, 128)
+    idx = np.abs(g).argmax(-1)
+    q_ext = np.take_along_axis(deq.reshape(64, 4, 128), idx[..., None], -1)[..., 0] / s16
+    assert np.all(np.abs(np.abs(q_ext) - 7) < 1e-6)
+
+
+def test_dequant_layout_low_nibble_is_even_k():
+    packed = np.array([[0x9F, 0x18]], dtype=np.uint8)  # k0=15, k1=9, k2=8, k3=1
+    scales = np.array([[2.0]], dtype=np.float16)
+    deq = quant.dequant_int4(packed, scales)
+    assert deq.tolist() == [[14.0, 2.0, 0.0, -14.0]]
+
+
+def test_expert_byte_counts_match_reference():
+    # Reference: INT4 bytes per expert = 3*H*I/2 (tests/test_stress.py:770, 796),
+    # plus fp16 scales = 3,244,032 (OLMoE) / 2,433,024 (Qwen3).
+    for H, I, wbytes, total in [(2048, 1024, 3145728, 3244032), (2048, 768, 2359296, 2433024)]:
+        w13 = np.zeros((1, 2 * I, H), np.float16)
+        w2 = np.zeros((1, H, I), np.float16)
+        p13, s13 = quant.pack_experts_int4(w13)
+        p2, s2 = quant.pack_experts_int4(w2)
+        assert p13.nbytes + p2.nbytes == wbytes
+        assert p13.nbytes + p2.nbytes + s13.nbytes + s2.nbytes == total
+        assert quant.int4_expert_bytes(H, I) == total
+
+
+def test_int8_known_answers_and_zero_rows():
+    w = np.zeros((2, 8), np.float32)
+    w[0, :4] = [127.0, -63.5, 0.5, 1.5]
+    q, s = quant.quantize_int8(w)
+    assert s[0] == np.float16(1.0)
+    assert q[0, :4].tolist() == [127, -64, 0, 2]
+    assert np.all(q[1] == 0)
+    # reference test_eval.py:158-163: zero rows stay finite and exact
+    z = np.zeros((4, 128), np.float16)
+    fz = quant.fake_quant_int8(z)
+    assert np.all(np.isfinite(fz)) and np.array_equal(fz, z)
+    assert np.array_equal(quant.dequant_int8(*quant.quantize_int8(z)), z.astype(np.float32))
+
+
+def test_fake_quant_int4_zero_rows_and_agreement():
+    z = np.zeros((4, 128), np.float16)
+    fz = quant.fake_quant_int4(z)  # reference test_eval.py:151-155
+    assert np.all(np.isfinite(fz)) and np.array_equal(fz, z)
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((8, 256)) * 0.02).astype(np.float16)
+    fq = quant.fake_quant_int4(w).astype(np.float32)
+    p, s = quant.pack_int4_weights(w)
+    deq = quant.dequant_int4(p, s)
+    # same integers; only the fp16 rounding of the scale differs (<= 2^-11 rel)
+    assert np.allclose(fq, deq, rtol=2e-3, atol=1e-6)
