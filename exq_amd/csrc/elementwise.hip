@@ -56,7 +56,8 @@ __global__ void inverse_perm_kernel(const int64_t* __restrict__ order, int n,
 __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ down, int dtype,
                                                       const int32_t* __restrict__ inv,
                                                       const void* __restrict__ w, int wdtype,
-                                                      int top_k, int H, void* __restrict__ out) {
+                                                      int top_k, int H, int n_rows,
+                                                      void* __restrict__ out) {
   const int t = blockIdx.y;
   const int h = blockIdx.x * blockDim.x + threadIdx.x;
   if (h >= H) return;
@@ -64,6 +65,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ d
   for (int j = 0; j < top_k; ++j) {
     const int64_t slot = (int64_t)t * top_k + j;
     const int i = inv[slot];
+    if (i < 0 || i >= n_rows) continue;  // sort_order was not a permutation
     acc += load_as_f32(w, wdtype, slot) * load_as_f32(down, dtype, (int64_t)i * H + h);
   }
   store_from_f32(out, dtype, (int64_t)t * H + h, acc);
@@ -153,7 +155,7 @@ extern "C" int exq_combine(const void* down_out, int dtype, const int64_t* sort_
   if (st) return st;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)cdiv(hidden_size, 256), (unsigned)n_tokens),
                      dim3(256), 0, s, down_out, dtype, inv, router_weights, weights_dtype,
-                     (int)top_k, (int)hidden_size, result);
+                     (int)top_k, (int)hidden_size, (int)n_active, result);
   return check_launch("combine_kernel");
 }
 

@@ -148,8 +148,10 @@ __global__ void __launch_bounds__(RT) build_ends_kernel(const int32_t* sid, int 
   if (threadIdx.x == 0) s.start[E] = t;
   __syncthreads();
   for (int e = threadIdx.x; e <= E; e += RT) ends[e] = s.start[e];
-  stable_scatter(em, E, key, s.run, s.masks,
-                 [&](int i, int, int pos) { sort_order[pos] = sid[i]; });
+  // A slot listed twice would overflow sort_order; such entries are dropped.
+  stable_scatter(em, E, key, s.run, s.masks, [&](int i, int, int pos) {
+    if (pos < n_active) sort_order[pos] = sid[i];
+  });
 }
 
 // ---- exq_moe_align_block_size ----------------------------------------------

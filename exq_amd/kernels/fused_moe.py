@@ -108,7 +108,17 @@ def quantize_int8_rows(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
     ``w [..., N, K]`` -> ``(q int8 [..., N, K], scales fp16 [..., N])``; the
     scale is max|w|/127 in fp32 (floored at fp32 eps), stored as fp16.
+    Device tensors are quantised by the HIP kernel.
     """
+    if w.is_cuda:
+        flat = w.reshape(-1, w.shape[-1]).contiguous()
+        dev = _lib.require_gpu(flat)
+        q = torch.empty(flat.shape, dtype=torch.int8, device=dev)
+        s = torch.empty(flat.shape[0], dtype=torch.float16, device=dev)
+        _lib.check(_lib.lib().exq_quantize_int8(
+            flat.data_ptr(), _lib.dtype_code(flat.dtype), flat.shape[0], flat.shape[1],
+            q.data_ptr(), s.data_ptr(), _lib.stream_handle(dev)), "quantize_int8")
+        return q.view(w.shape), s.view(w.shape[:-1])
     w32 = w.to(torch.float32)
     scale = torch.clamp_min(w32.abs().amax(dim=-1, keepdim=True) / 127.0, _EPS)
     q = torch.round(w32 / scale).clamp_(-128, 127).to(torch.int8)

@@ -46,15 +46,31 @@ def _pack_rows(w: torch.Tensor, group_size: int) -> tuple[torch.Tensor, torch.Te
     return packed, scale.to(torch.float16)
 
 
+def _pack_gpu(flat: torch.Tensor, K: int, g: int) -> tuple[torch.Tensor, torch.Tensor]:
+    rows = flat.shape[0]
+    dev = _lib.require_gpu(flat)
+    packed = torch.empty(rows, K // 2, dtype=torch.uint8, device=dev)
+    scales = torch.empty(rows, K // g, dtype=torch.float16, device=dev)
+    L = _lib.lib()
+    _lib.check(L.exq_pack_int4(flat.data_ptr(), _lib.dtype_code(flat.dtype), rows, K, g,
+                               packed.data_ptr(), scales.data_ptr(), _lib.stream_handle(dev)),
+               "pack_int4")
+    return packed, scales
+
+
 def pack_int4_weights(weights: torch.Tensor, group_size: int = 128
                       ) -> tuple[torch.Tensor, torch.Tensor]:
     """Pack [N, K] weights to INT4 with per-group fp16 scales (RTN, symmetric).
 
     Returns ``(packed uint8 [N, K//2], scales fp16 [N, K//g])``.  Raises
-    ValueError if K is odd or not divisible by the group size.
+    ValueError if K is odd or not divisible by the group size.  Device
+    tensors are packed by the HIP kernel; host tensors with torch CPU ops
+    (same arithmetic, for offline packing).
     """
     N, K = weights.shape
     g = _group_rule(K, group_size)
+    if weights.is_cuda:
+        return _pack_gpu(weights.contiguous(), K, g)
     packed, scales = _pack_rows(weights, g)
     return packed.contiguous(), scales.contiguous()
 
@@ -63,12 +79,15 @@ def pack_experts_int4(expert_weights: torch.Tensor, group_size: int = 128,
                       rows_per_chunk: int = 1 << 16) -> tuple[torch.Tensor, torch.Tensor]:
     """Pack an [E, N, K] bank: ``(packed [E, N, K//2], scales [E, N, K//g])``.
 
-    Rows are independent, so the bank is packed in row chunks (bounded fp32
-    temporaries) rather than one expert at a time.
+    Device banks go through the HIP kernel in one launch; host banks are
+    packed with torch CPU ops in row chunks (bounded fp32 temporaries).
     """
     E, N, K = expert_weights.shape
     g = _group_rule(K, group_size)
     flat = expert_weights.reshape(E * N, K)
+    if flat.is_cuda:
+        p, s = _pack_gpu(flat.contiguous(), K, g)
+        return p.view(E, N, K // 2), s.view(E, N, K // g)
     packed = torch.empty(E * N, K // 2, dtype=torch.uint8, device=expert_weights.device)
     scales = torch.empty(E * N, K // g, dtype=torch.float16, device=expert_weights.device)
     for r0 in range(0, E * N, rows_per_chunk):

@@ -166,6 +166,27 @@ int exq_moe_grouped_gemm(const void* a_sorted, int act_dtype, int64_t n_rows, in
                          const int32_t* expert_ends, const int32_t* expert_mask,
                          void* c, void* workspace, size_t workspace_bytes, exq_stream stream);
 
+/* ---- weight quantisation -------------------------------------------------- */
+
+/*
+ * INT4 RTN packing of [rows, K] weights (f32 | f16 | bf16), bit-exact with
+ * pack_int4_weights / pack_experts_int4 (exq/kernels/moe_int4_kernel.py:37-119):
+ * per (row, group) scale = max|w| / 7 in fp32 (IEEE division) floored at fp32
+ * eps, q = round-half-even(w / scale) clamped to [-8, 7], nibble q + 8 (even k
+ * low), scales stored fp16.  K < group_size collapses to one group of K.
+ * Replaces the one-time packing of _get_or_pack (sglang_backend.py:32-60).
+ */
+int exq_pack_int4(const void* weights, int dtype, int64_t rows, int64_t K,
+                  int64_t group_size, uint8_t* packed, uint16_t* scales, exq_stream stream);
+
+/*
+ * INT8 per-output-row RTN (exq/eval/quant_shim.py:84-96 rule): scale =
+ * max|w| / 127 (fp32, floored at eps), q = round-half-even(w / scale) clamped
+ * to [-128, 127]; the scale is stored fp16.
+ */
+int exq_quantize_int8(const void* weights, int dtype, int64_t rows, int64_t K, int8_t* q,
+                      uint16_t* scales, exq_stream stream);
+
 /* ---- fused MoE layer ----------------------------------------------------- */
 
 typedef struct exq_moe_problem {

@@ -44,6 +44,24 @@ def test_pack_on_gpu_bit_exact(device):
     rp, rs = quant.pack_experts_int4(w)
     assert np.array_equal(p.cpu().numpy(), rp)
     assert np.array_equal(s.cpu().numpy(), rs)
+    # K < g collapses to g = K = 96 (serial kernel); bf16 and f32 inputs
+    for arr, tdt in [(w[:, :8, :96], torch.float16), (w[:, :8, :512], torch.bfloat16),
+                     (w[:, :8, :256], torch.float32)]:
+        t = torch.from_numpy(arr.astype(np.float32)).to(tdt)
+        p, s = pack_experts_int4(t.to(device))
+        rp, rs = quant.pack_experts_int4(t.float().numpy())
+        assert np.array_equal(p.cpu().numpy(), rp) and np.array_equal(s.cpu().numpy(), rs)
+
+
+def test_quantize_int8_on_gpu_bit_exact(device):
+    from exq_amd.kernels import quantize_int8_rows
+    banner("quantize_int8_rows on GPU")
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((3, 64, 1000)) * 0.02).astype(np.float16)
+    w[2, 5] = 0
+    q, s = quantize_int8_rows(torch.from_numpy(w).to(device))
+    rq, rs = quant.quantize_int8(w)
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), rs)
 
 
 SMALL = synth.MoeConfig("small", 9, 256, 128, 4, 2, False)
