@@ -52,4 +52,15 @@ int launch_route_plan(const RoutePlanParams& p, hipStream_t stream);
 int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, int tier,
                         int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream);
 
+// Self-routing decode kernels (decode.hip).  mode 0: gate/up + SiLU into mid
+// rows indexed by slot t*kp + j; mode 1: down projection into fp32 partial
+// rows indexed the same way.
+bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared);
+int launch_decode(bool bf, int mode, const void* ids, int ids_dtype, int T, int k, int kp,
+                  int E, int Ep, const uint16_t* x, int64_t x_stride, int K,
+                  const int8_t* tier, const int32_t* index, const uint16_t* bf16,
+                  const int8_t* i8, const uint16_t* i8_scales, const uint8_t* i4,
+                  const uint16_t* i4_scales, int n_rows, int inter, int group_size, void* out,
+                  int64_t out_stride, int n_blocks, hipStream_t s);
+
 }  // namespace exq

@@ -57,14 +57,6 @@ struct GemmArgs {
   int group_size;          // INT4 group size, multiple of 128
   void* out;               // GATEUP mid [n, I] act | PLAIN C [rows, N] act | DOWN partial [n, H] f32
   int64_t out_stride;
-  // DOWN: last-arriver combine into final_out [T, H]
-  int* counters;
-  const void* ids;
-  int ids_dtype;
-  const void* topk_w;
-  int w_dtype;
-  int T, k, kp, E;
-  uint16_t* final_out;
   int H;
 };
 
@@ -147,7 +139,7 @@ struct WBuf {
 
 template <int TIER, bool BF, int MODE>
 __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TgEntry& te, int blk,
-                                          int n_tg, unsigned char* lds) {
+                                          unsigned char* lds) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, kq = lane >> 4;
   const int cnt = te.cnt;
@@ -393,45 +385,6 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TgEntry& te, 
     }
   }
 
-  if constexpr (MODE == MODE_DOWN) {
-    // Last work-group to finish this block of 32 output columns sums the
-    // partial rows of every token in the fixed slot order j = 0..kp-1.
-    __threadfence();
-    __syncthreads();
-    int* flag = reinterpret_cast<int*>(lds);
-    if (tid == 0) {
-      const int old = atomicAdd(&a.counters[blk], 1);
-      flag[0] = (old == n_tg - 1) ? 1 : 0;
-    }
-    __syncthreads();
-    if (flag[0]) {
-      __threadfence();
-      const float* part = reinterpret_cast<const float*>(a.out);
-      for (int idx = tid; idx < a.T * 8; idx += NTH) {
-        const int t = idx >> 3;
-        const int h = blk * 32 + (idx & 7) * 4;
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < a.kp; ++j) {
-          float wgt = 1.f;
-          if (j < a.k) {
-            const int64_t id = load_index(a.ids, a.ids_dtype, (int64_t)t * a.k + j);
-            if (id < 0 || id >= a.E) continue;
-            wgt = load_as_f32(a.topk_w, a.w_dtype, (int64_t)t * a.k + j);
-          }
-          const float4 pv = *reinterpret_cast<const float4*>(
-              part + ((int64_t)t * a.kp + j) * a.out_stride + h);
-          acc[0] += wgt * pv.x;
-          acc[1] += wgt * pv.y;
-          acc[2] += wgt * pv.z;
-          acc[3] += wgt * pv.w;
-        }
-        uint2 o;
-        o.x = to_act_bits<BF>(acc[0]) | (to_act_bits<BF>(acc[1]) << 16);
-        o.y = to_act_bits<BF>(acc[2]) | (to_act_bits<BF>(acc[3]) << 16);
-        *reinterpret_cast<uint2*>(a.final_out + (int64_t)t * a.H + h) = o;
-      }
-    }
-  }
 }
 
 template <bool BF, int MODE>
@@ -450,12 +403,47 @@ __global__ void __launch_bounds__(NTH, 2) moe_gemm_kernel(GemmArgs a) {
   const int blk = unit - tgi * a.n_blocks;
   const TgEntry te = a.tg[tgi];
   if (te.tier == 0) {
-    gemm_body<0, BF, MODE>(a, te, blk, n_tg, lds);
+    gemm_body<0, BF, MODE>(a, te, blk, lds);
   } else if (te.tier == 1) {
-    gemm_body<1, BF, MODE>(a, te, blk, n_tg, lds);
+    gemm_body<1, BF, MODE>(a, te, blk, lds);
   } else {
-    gemm_body<2, BF, MODE>(a, te, blk, n_tg, lds);
+    gemm_body<2, BF, MODE>(a, te, blk, lds);
   }
+}
+
+// out[t, h] = sum_j w[t, j] * partial[t*kp + j, h] over the routed slots that
+// were not dropped (shared-expert slots j >= k have weight 1), fp32 in the
+// fixed order j = 0..kp-1, rounded once to the activation dtype.  One thread
+// per 4 consecutive h.  A separate launch: the kernel boundary makes every
+// partial row visible without a device-wide fence in the down kernel.
+template <bool BF>
+__global__ void __launch_bounds__(256) combine_partials_kernel(
+    const float* __restrict__ part, const void* __restrict__ ids, int ids_dtype,
+    const void* __restrict__ topk_w, int w_dtype, int T, int k, int kp, int E, int H,
+    uint16_t* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int hq = H >> 2;
+  if (idx >= (int64_t)T * hq) return;
+  const int t = (int)(idx / hq);
+  const int h = (int)(idx - (int64_t)t * hq) * 4;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < kp; ++j) {
+    float wgt = 1.f;
+    if (j < k) {
+      const int64_t id = load_index(ids, ids_dtype, (int64_t)t * k + j);
+      if (id < 0 || id >= E) continue;
+      wgt = load_as_f32(topk_w, w_dtype, (int64_t)t * k + j);
+    }
+    const float4 pv = *reinterpret_cast<const float4*>(part + ((int64_t)t * kp + j) * H + h);
+    acc[0] += wgt * pv.x;
+    acc[1] += wgt * pv.y;
+    acc[2] += wgt * pv.z;
+    acc[3] += wgt * pv.w;
+  }
+  uint2 o;
+  o.x = to_act_bits<BF>(acc[0]) | (to_act_bits<BF>(acc[1]) << 16);
+  o.y = to_act_bits<BF>(acc[2]) | (to_act_bits<BF>(acc[3]) << 16);
+  *reinterpret_cast<uint2*>(out + (int64_t)t * H + h) = o;
 }
 
 template <int MODE>
@@ -486,7 +474,7 @@ int record_stage(int i, hipStream_t s) {
 
 // ---- workspace layout of the fused forward --------------------------------------
 struct FusedLayout {
-  size_t hdr, ends, sorted, tg, counters, mid, partial, total;
+  size_t hdr, ends, sorted, tg, mid, partial, total;
   int64_t n, tg_cap;
 };
 
@@ -501,7 +489,6 @@ FusedLayout fused_layout(const exq_moe_problem& p) {
   L.ends = off;     off = align_up(off + (size_t)(Ep + 1) * 4, 256);
   L.sorted = off;   off = align_up(off + (size_t)L.n * 4, 256);
   L.tg = off;       off = align_up(off + (size_t)L.tg_cap * sizeof(TgEntry), 256);
-  L.counters = off; off = align_up(off + (size_t)(p.hidden_size / 32 + 1) * 4, 256);
   L.mid = off;      off = align_up(off + (size_t)L.n * p.inter_size * 2, 256);
   L.partial = off;  off = align_up(off + (size_t)L.n * p.hidden_size * 4, 256);
   L.total = off;
@@ -568,8 +555,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   rp.sorted = reinterpret_cast<int*>(ws + L.sorted);
   rp.tg = reinterpret_cast<TgEntry*>(ws + L.tg);
   rp.tg_cap = (int)L.tg_cap;
-  rp.counters = reinterpret_cast<int*>(ws + L.counters);
-  rp.n_counters = H / 32;
+  rp.counters = nullptr;
+  rp.n_counters = 0;
   rp.sort_order_out = sort_order_out;
   rp.ends_out = expert_ends_out;
   rp.out = out;
@@ -577,52 +564,77 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   struct HookReset {  // the hook is consumed by this call, whatever happens
     ~HookReset() { g_stage_events_set = false; }
   } hook_reset;
+  const bool decode = decode_path_supported(T, k, Ep, p->n_shared);
   int st = record_stage(0, s);
   if (st) return st;
-  st = launch_route_plan(rp, s);
-  if (st) return st;
+  // The decode path routes inside its GEMM waves; the routing plan runs only
+  // when the caller asked for the routing arrays.
+  if (!decode || sort_order_out || expert_ends_out) {
+    st = launch_route_plan(rp, s);
+    if (st) return st;
+  }
   st = record_stage(1, s);
   if (st) return st;
 
-  GemmArgs g{};
-  g.hdr = rp.hdr;
-  g.tg = rp.tg;
-  g.row_slot = rp.sorted;
-  g.slot_div = kp;
-  g.group_size = (int)p->group_size;
-  g.inter = I;
-  // gate/up + SiLU: x = hidden, K = H, rows = 2I, out = mid [n, I]
-  g.n_blocks = I / 16;
-  g.x = reinterpret_cast<const uint16_t*>(hidden);
-  g.x_stride = H;
-  g.K = H;
-  g.w = b13;
-  g.n_rows = 2 * I;
-  g.out = ws + L.mid;
-  g.out_stride = I;
-  st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
-  if (st) return st;
-  st = record_stage(2, s);
-  if (st) return st;
-
-  // down + combine: x = mid rows (expert-sorted), K = I, rows = H
-  g.n_blocks = H / 32;
-  g.x = reinterpret_cast<const uint16_t*>(ws + L.mid);
-  g.x_stride = I;
-  g.K = I;
-  g.w = b2;
-  g.n_rows = H;
-  g.out = ws + L.partial;
-  g.out_stride = H;
-  g.counters = rp.counters;
-  g.ids = topk_ids;
-  g.ids_dtype = p->ids_dtype;
-  g.topk_w = topk_weights;
-  g.w_dtype = p->weights_dtype;
-  g.T = T; g.k = k; g.kp = kp; g.E = E;
-  g.final_out = reinterpret_cast<uint16_t*>(out);
-  g.H = H;
-  st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
+  if (decode) {
+    st = launch_decode(bf, 0, topk_ids, p->ids_dtype, T, k, kp, E, Ep,
+                       reinterpret_cast<const uint16_t*>(hidden), H, H, b13.tier, b13.index,
+                       b13.bf16, b13.i8, b13.i8_scales, b13.i4, b13.i4_scales, 2 * I, I,
+                       (int)p->group_size, ws + L.mid, I, I / 16, s);
+    if (st) return st;
+    st = record_stage(2, s);
+    if (st) return st;
+    st = launch_decode(bf, 1, topk_ids, p->ids_dtype, T, k, kp, E, Ep,
+                       reinterpret_cast<const uint16_t*>(ws + L.mid), I, I, b2.tier, b2.index,
+                       b2.bf16, b2.i8, b2.i8_scales, b2.i4, b2.i4_scales, H, I,
+                       (int)p->group_size, ws + L.partial, H, H / 32, s);
+    if (st) return st;
+  } else {
+    GemmArgs g{};
+    g.hdr = rp.hdr;
+    g.tg = rp.tg;
+    g.row_slot = rp.sorted;
+    g.slot_div = kp;
+    g.group_size = (int)p->group_size;
+    g.inter = I;
+    // gate/up + SiLU: x = hidden, K = H, rows = 2I, out = mid [n, I] (sorted rows)
+    g.n_blocks = I / 16;
+    g.x = reinterpret_cast<const uint16_t*>(hidden);
+    g.x_stride = H;
+    g.K = H;
+    g.w = b13;
+    g.n_rows = 2 * I;
+    g.out = ws + L.mid;
+    g.out_stride = I;
+    st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
+    if (st) return st;
+    st = record_stage(2, s);
+    if (st) return st;
+    // down: x = mid rows (expert-sorted), K = I, rows = H, out = partial [slot, H]
+    g.n_blocks = H / 32;
+    g.x = reinterpret_cast<const uint16_t*>(ws + L.mid);
+    g.x_stride = I;
+    g.K = I;
+    g.w = b2;
+    g.n_rows = H;
+    g.out = ws + L.partial;
+    g.out_stride = H;
+    g.H = H;
+    st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
+    if (st) return st;
+  }
+  const int64_t threads = (int64_t)T * (H / 4);
+  if (bf)
+    hipLaunchKernelGGL(combine_partials_kernel<true>, dim3((unsigned)cdiv(threads, 256)),
+                       dim3(256), 0, s, reinterpret_cast<const float*>(ws + L.partial),
+                       topk_ids, p->ids_dtype, topk_weights, p->weights_dtype, T, k, kp, E, H,
+                       reinterpret_cast<uint16_t*>(out));
+  else
+    hipLaunchKernelGGL(combine_partials_kernel<false>, dim3((unsigned)cdiv(threads, 256)),
+                       dim3(256), 0, s, reinterpret_cast<const float*>(ws + L.partial),
+                       topk_ids, p->ids_dtype, topk_weights, p->weights_dtype, T, k, kp, E, H,
+                       reinterpret_cast<uint16_t*>(out));
+  st = check_launch("combine_partials_kernel");
   if (st) return st;
   return record_stage(3, s);
 }

@@ -262,7 +262,8 @@ int exq_moe_mixed_forward(const exq_moe_problem* problem, const void* hidden,
  * calls with perf_counter, exq/eval/bench.py:15-46).  When set on the calling
  * thread, the next fused / mixed forward records events[0] before the routing
  * kernel, events[1] before the gate/up kernel, events[2] before the down
- * kernel and events[3] after it, on the call's stream.  events are hipEvent_t
+ * kernel and events[3] after the combine kernel that follows it, on the
+ * call's stream.  events are hipEvent_t
  * handles; pass (NULL, 0) to disable.  The hook is consumed by one call.
  */
 int exq_set_stage_events(void* const* events, int n_events);
