@@ -144,13 +144,52 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// LDS budget for the staged activation rows of one work-group.
+constexpr int X_LDS_BUDGET = 72 * 1024;
+
+// Stage activation rows [0, nrows) x k in [k0, k0 + kc) into LDS (row stride
+// kc_alloc + 8 halfs); INT4 experts get the (0,4,1,5,2,6,3,7) order that
+// matches the nibble expansion.
+template <int MODE>
+__device__ __noinline__ void stage_rows(const DecodeArgs& a, const int* row_slot, int nrows,
+                                        int k0, int kc, int xstride, bool int4_order,
+                                        uint16_t* xs) {
+  const int ppr = kc >> 3;  // 16-byte pieces per row
+  const int total = nrows * ppr;
+  for (int base = threadIdx.x; base < total; base += DNT * 4) {
+    uint4 v[4];
+    int dst[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int pidx = base + u * DNT;
+      dst[u] = -1;
+      if (pidx < total) {
+        const int m = pidx / ppr;
+        const int q = pidx - m * ppr;
+        const int slot = row_slot[m];
+        const int64_t row = MODE == D_GATEUP ? (int64_t)(slot / a.kp) : (int64_t)slot;
+        v[u] = *reinterpret_cast<const uint4*>(a.x + row * a.x_stride + k0 + q * 8);
+        dst[u] = m * xstride + q * 8;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (dst[u] >= 0)
+        *reinterpret_cast<uint4*>(xs + dst[u]) = int4_order ? dperm(v[u]) : v[u];
+    }
+  }
+}
+
 template <int TIER, bool BF, int MODE, int NT, int P>
-__device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, int cnt,
-                                            const int* slot_of_row /*[NT] per lane*/) {
+__device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, bool active,
+                                            int cnt, const int* row_slot, int kc,
+                                            uint16_t* xs) {
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15, kq = lane >> 4;
   const int ntiles = (cnt + 15) >> 4;
   const int nkb = a.K >> 7;
+  const int kcb = kc >> 7;            // k-blocks per staged chunk
+  const int xstride = kc + 8;         // halfs per staged row
 
   int rows[2];
   if (MODE == D_GATEUP) {
@@ -162,40 +201,27 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
   }
   const int widx = a.w.index ? a.w.index[e] : e;
   const int64_t ebase = (int64_t)widx * a.n_rows;
-  const unsigned char* rp[2];
+  const unsigned char* rp[2] = {nullptr, nullptr};
   const uint16_t* sp[2] = {nullptr, nullptr};
   float rowscale[2] = {1.f, 1.f};
   const int ngs = TIER == 2 ? a.K / a.group_size : 1;
+  if (active) {
 #pragma unroll
-  for (int rs = 0; rs < 2; ++rs) {
-    const int64_t r = ebase + rows[rs];
-    if constexpr (TIER == 2) {
-      rp[rs] = a.w.i4 + r * (a.K / 2) + kq * 16;
-      sp[rs] = a.w.i4_scales + r * ngs;
-    } else if constexpr (TIER == 1) {
-      rp[rs] = reinterpret_cast<const unsigned char*>(a.w.i8) + r * a.K + kq * 32;
-      rowscale[rs] = f16_bits_to_f32(a.w.i8_scales[r]);
-    } else {
-      rp[rs] = reinterpret_cast<const unsigned char*>(a.w.bf16 + r * a.K) + kq * 64;
+    for (int rs = 0; rs < 2; ++rs) {
+      const int64_t r = ebase + rows[rs];
+      if constexpr (TIER == 2) {
+        rp[rs] = a.w.i4 + r * (a.K / 2) + kq * 16;
+        sp[rs] = a.w.i4_scales + r * ngs;
+      } else if constexpr (TIER == 1) {
+        rp[rs] = reinterpret_cast<const unsigned char*>(a.w.i8) + r * a.K + kq * 32;
+        rowscale[rs] = f16_bits_to_f32(a.w.i8_scales[r]);
+      } else {
+        rp[rs] = reinterpret_cast<const unsigned char*>(a.w.bf16 + r * a.K) + kq * 64;
+      }
     }
   }
-  // bytes per lane per k-block and row set
-  constexpr int BPK = TIER == 2 ? 16 : (TIER == 1 ? 32 : 64);
-  constexpr int QPK = BPK / 16;  // uint4 per lane per k-block and row set
+  constexpr int QPK = TIER == 2 ? 1 : (TIER == 1 ? 2 : 4);  // uint4 per lane, k-block, row set
   constexpr int KBSTRIDE = TIER == 2 ? 64 : (TIER == 1 ? 128 : 256);  // row bytes per k-block
-
-  // activation row pointers for this lane's A-operand rows (one per tile)
-  const uint16_t* xrow[NT];
-#pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    const int q = tt * 16 + r16;
-    xrow[tt] = nullptr;
-    if (q < cnt) {
-      const int slot = slot_of_row[tt];
-      const int64_t row = MODE == D_GATEUP ? (int64_t)(slot / a.kp) : (int64_t)slot;
-      xrow[tt] = a.x + row * a.x_stride + kq * 32;
-    }
-  }
 
   uint4 wq[P][2][QPK];
   uint32_t wsc[P][2];
@@ -208,9 +234,12 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
       if constexpr (TIER == 2) wsc[slotp][rs] = sp[rs][(kb * 128) / a.group_size];
     }
   };
+  // Weight stream first: its HBM latency overlaps the activation staging.
+  if (active) {
 #pragma unroll
-  for (int p = 0; p < P; ++p)
-    if (p < nkb) load_w(p, p);
+    for (int p = 0; p < P; ++p)
+      if (p < nkb) load_w(p, p);
+  }
 
   f32x4_t tot0[NT], tot1[NT];
 #pragma unroll
@@ -219,94 +248,97 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
     tot1[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const uint4 negb = neg_base_operand<TIER, BF>();
+  // A-operand rows beyond cnt read row cnt-1: finite values whose outputs are dropped.
+  int arow[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int q = tt * 16 + r16;
+    arow[tt] = (q < cnt ? q : cnt - 1) * xstride + kq * 32;
+  }
 
   for (int kb0 = 0; kb0 < nkb; kb0 += P) {
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       const int kb = kb0 + p;
       if (kb < nkb) {
-        // activation fragments (16x32 A operand per MFMA step d)
-        uint4 xa[NT][4];
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-#pragma unroll
-          for (int d = 0; d < 4; ++d) xa[tt][d] = uint4{0u, 0u, 0u, 0u};
-          if (tt < ntiles && xrow[tt] != nullptr) {
-            const uint4* src = reinterpret_cast<const uint4*>(xrow[tt] + kb * 128);
-#pragma unroll
-            for (int d = 0; d < 4; ++d) xa[tt][d] = src[d];
-            if constexpr (TIER == 2) {
-#pragma unroll
-              for (int d = 0; d < 4; ++d) xa[tt][d] = dperm(xa[tt][d]);
-            }
-          }
+        if (kb % kcb == 0) {  // next staged chunk (uniform across the work-group)
+          if (kb > 0) __syncthreads();
+          const int k0 = kb * 128;
+          const int kcc = a.K - k0 < kc ? a.K - k0 : kc;
+          stage_rows<MODE>(a, row_slot, cnt, k0, kcc, xstride, TIER == 2, xs);
+          __syncthreads();
         }
-        // weights -> B operands
-        uint4 bfr[2][4];
-        float sc[2] = {1.f, 1.f};
+        if (active) {
+          uint4 bfr[2][4];
+          float sc[2] = {1.f, 1.f};
 #pragma unroll
-        for (int rs = 0; rs < 2; ++rs) {
-          if constexpr (TIER == 2) {
-            const uint4 w = wq[p][rs][0];
-            bfr[rs][0] = ddeq4<BF>(w.x);
-            bfr[rs][1] = ddeq4<BF>(w.y);
-            bfr[rs][2] = ddeq4<BF>(w.z);
-            bfr[rs][3] = ddeq4<BF>(w.w);
-            sc[rs] = f16_bits_to_f32(wsc[p][rs]);
-          } else if constexpr (TIER == 1) {
-            const uint4 w0 = wq[p][rs][0], w1 = wq[p][rs][1];
-            const uint2 d0 = ddeq8<BF>(w0.x), d1 = ddeq8<BF>(w0.y);
-            const uint2 d2 = ddeq8<BF>(w0.z), d3 = ddeq8<BF>(w0.w);
-            const uint2 d4 = ddeq8<BF>(w1.x), d5 = ddeq8<BF>(w1.y);
-            const uint2 d6 = ddeq8<BF>(w1.z), d7 = ddeq8<BF>(w1.w);
-            bfr[rs][0] = uint4{d0.x, d0.y, d1.x, d1.y};
-            bfr[rs][1] = uint4{d2.x, d2.y, d3.x, d3.y};
-            bfr[rs][2] = uint4{d4.x, d4.y, d5.x, d5.y};
-            bfr[rs][3] = uint4{d6.x, d6.y, d7.x, d7.y};
-          } else {
-#pragma unroll
-            for (int h = 0; h < 4; ++h) bfr[rs][h] = wq[p][rs][h];
-          }
-        }
-        // refill this ring slot
-        if (kb + P < nkb) load_w(p, kb + P);
-#pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-          if (tt < ntiles) {
-            f32x4_t init = {0.f, 0.f, 0.f, 0.f};
-            if constexpr (TIER != 0) {
-#pragma unroll
-              for (int d = 0; d < 4; ++d) init = dmfma<BF>(xa[tt][d], negb, init);
-            }
-            f32x4_t acc0 = init, acc1 = init;
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              acc0 = dmfma<BF>(xa[tt][d], bfr[0][d], acc0);
-              acc1 = dmfma<BF>(xa[tt][d], bfr[1][d], acc1);
-            }
+          for (int rs = 0; rs < 2; ++rs) {
             if constexpr (TIER == 2) {
-              tot0[tt] += sc[0] * acc0;
-              tot1[tt] += sc[1] * acc1;
+              const uint4 w = wq[p][rs][0];
+              bfr[rs][0] = ddeq4<BF>(w.x);
+              bfr[rs][1] = ddeq4<BF>(w.y);
+              bfr[rs][2] = ddeq4<BF>(w.z);
+              bfr[rs][3] = ddeq4<BF>(w.w);
+              sc[rs] = f16_bits_to_f32(wsc[p][rs]);
+            } else if constexpr (TIER == 1) {
+              const uint4 w0 = wq[p][rs][0], w1 = wq[p][rs][1];
+              const uint2 d0 = ddeq8<BF>(w0.x), d1 = ddeq8<BF>(w0.y);
+              const uint2 d2 = ddeq8<BF>(w0.z), d3 = ddeq8<BF>(w0.w);
+              const uint2 d4 = ddeq8<BF>(w1.x), d5 = ddeq8<BF>(w1.y);
+              const uint2 d6 = ddeq8<BF>(w1.z), d7 = ddeq8<BF>(w1.w);
+              bfr[rs][0] = uint4{d0.x, d0.y, d1.x, d1.y};
+              bfr[rs][1] = uint4{d2.x, d2.y, d3.x, d3.y};
+              bfr[rs][2] = uint4{d4.x, d4.y, d5.x, d5.y};
+              bfr[rs][3] = uint4{d6.x, d6.y, d7.x, d7.y};
             } else {
-              tot0[tt] += acc0;
-              tot1[tt] += acc1;
+#pragma unroll
+              for (int h = 0; h < 4; ++h) bfr[rs][h] = wq[p][rs][h];
+            }
+          }
+          if (kb + P < nkb) load_w(p, kb + P);  // refill this ring slot
+          const int koff = (kb % kcb) * 128;
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt) {
+            if (tt < ntiles) {
+              uint4 xa[4];
+#pragma unroll
+              for (int d = 0; d < 4; ++d)
+                xa[d] = *reinterpret_cast<const uint4*>(xs + arow[tt] + koff + d * 8);
+              f32x4_t init = {0.f, 0.f, 0.f, 0.f};
+              if constexpr (TIER != 0) {
+#pragma unroll
+                for (int d = 0; d < 4; ++d) init = dmfma<BF>(xa[d], negb, init);
+              }
+              f32x4_t acc0 = init, acc1 = init;
+#pragma unroll
+              for (int d = 0; d < 4; ++d) {
+                acc0 = dmfma<BF>(xa[d], bfr[0][d], acc0);
+                acc1 = dmfma<BF>(xa[d], bfr[1][d], acc1);
+              }
+              if constexpr (TIER == 2) {
+                tot0[tt] += sc[0] * acc0;
+                tot1[tt] += sc[1] * acc1;
+              } else {
+                tot0[tt] += acc0;
+                tot1[tt] += acc1;
+              }
             }
           }
         }
       }
     }
   }
+  if (!active) return;
 
   // Epilogue: lane holds rows (tokens) tt*16 + 4*kq + i, column r16.
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
     if (tt >= ntiles) continue;
-    const int slot_src = slot_of_row[tt];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int q = tt * 16 + kq * 4 + i;
-      const int slot = __shfl(slot_src, kq * 4 + i, 64);
       if (q >= cnt) continue;
+      const int slot = row_slot[q];
       const float g0 = tot0[tt][i] * rowscale[0], g1 = tot1[tt][i] * rowscale[1];
       if constexpr (MODE == D_GATEUP) {
         uint16_t* mid = reinterpret_cast<uint16_t*>(a.out);
@@ -323,8 +355,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
 }
 
 template <bool BF, int MODE, int NT>
-__global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a) {
+__global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a, int kc) {
+  extern __shared__ uint4 dyn_lds[];
   __shared__ uint32_t bitmap[DW][MAX_BM_WORDS];
+  __shared__ int row_slot[64 * MAX_ID_REGS];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = a.T * a.k;
   const int nw = (a.Ep + 31) >> 5;
@@ -341,7 +375,7 @@ __global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a) {
     }
     idr[i] = v;
   }
-  // 2. active-expert bitmap (per wave, in LDS)
+  // 2. active-expert bitmap (each wave builds its own copy in LDS)
   uint32_t* bm = bitmap[wave];
   if (lane < nw) bm[lane] = 0u;
   wave_lds_fence();
@@ -360,24 +394,24 @@ __global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a) {
   }
   const int n_active = __shfl(incl, 63, 64);
 
-  // 3. this wave's unit; work-group i runs on XCD i % 8, so each XCD takes a
-  //    contiguous range of units (the waves of one expert share its L2)
+  // 3. the work-group's unit (expert, group of 4 row blocks).  Work-group i
+  //    runs on XCD i % 8; each XCD takes a contiguous range of units.
   const int nbw = (a.n_blocks + DW - 1) / DW;
   const int U = n_active * nbw;
   const int per = (U + 7) >> 3;
   const int local = blockIdx.x >> 3;
   const int u = (blockIdx.x & 7) * per + local;
-  if (local >= per || u >= U) return;
+  if (local >= per || u >= U) return;  // uniform across the work-group
   const int ai = u / nbw;
   const int jb = (u - ai * nbw) * DW + wave;
-  if (jb >= a.n_blocks) return;
+  const bool active = jb < a.n_blocks;
 
   // 4. the ai-th active expert
   const uint64_t hit = __ballot(incl - c <= ai && ai < incl);
   const int wl = __ffsll((unsigned long long)hit) - 1;
   uint32_t wbits = __shfl(word, wl, 64);
-  int q = ai - (__shfl(incl, wl, 64) - __shfl(c, wl, 64));
-  for (int t = 0; t < q; ++t) wbits &= wbits - 1u;
+  const int q0 = ai - (__shfl(incl, wl, 64) - __shfl(c, wl, 64));
+  for (int t = 0; t < q0; ++t) wbits &= wbits - 1u;
   const int e = wl * 32 + (__ffs(wbits) - 1);
 
   // 5. the expert's slots in ascending order (extended slot t*kp + j)
@@ -393,48 +427,57 @@ __global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a) {
   } else {
     cnt = a.T;
   }
-  int slot_of_row[NT];
+  // Slot table in LDS.  A token routed twice to one expert (duplicate ids)
+  // simply adds rows; cnt <= T*k <= 1024.
+  if (wave == 0) {
+    for (int r0 = 0; r0 < cnt; r0 += 64) {
+      int r = r0 + lane;
+      if (r < cnt) {
+        int slot;
+        if (e < a.E) {
+          int s = 0;
 #pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    int r = tt * 16 + (lane & 15);
-    int slot = 0;
-    if (r < cnt) {
-      if (e < a.E) {
-        int s = 0;
-#pragma unroll
-        for (int i = 0; i < MAX_ID_REGS; ++i) {
-          const int ci = __popcll(m[i]);
-          if (r >= 0 && r < ci) s = 64 * i + nth_set_bit(m[i], r);
-          r -= ci;
+          for (int i = 0; i < MAX_ID_REGS; ++i) {
+            const int ci = __popcll(m[i]);
+            if (r >= 0 && r < ci) s = 64 * i + nth_set_bit(m[i], r);
+            r -= ci;
+          }
+          const int t = s / a.k;
+          slot = t * a.kp + (s - t * a.k);
+        } else {
+          slot = r * a.kp + a.k + (e - a.E);
         }
-        const int t = s / a.k;
-        slot = t * a.kp + (s - t * a.k);
-      } else {
-        slot = r * a.kp + a.k + (e - a.E);
+        row_slot[r0 + lane] = slot;
       }
     }
-    slot_of_row[tt] = slot;
   }
-  if (cnt > NT * 16) cnt = NT * 16;  // host guarantees T <= NT*16
+  __syncthreads();
 
+  uint16_t* xs = reinterpret_cast<uint16_t*>(dyn_lds);
   const int tier = a.w.tier ? (int)a.w.tier[e] : 2;
-  if (tier == 2) {
-    decode_body<2, BF, MODE, NT, 8>(a, e, jb, cnt, slot_of_row);
-  } else if (tier == 1) {
-    decode_body<1, BF, MODE, NT, 4>(a, e, jb, cnt, slot_of_row);
-  } else {
-    decode_body<0, BF, MODE, NT, 2>(a, e, jb, cnt, slot_of_row);
+  // Rows are processed 16*NT at a time (one pass unless ids repeat).
+  for (int r0 = 0; r0 < cnt; r0 += NT * 16) {
+    const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
+    if (tier == 2) {
+      decode_body<2, BF, MODE, NT, 8>(a, e, jb, active, cc, row_slot + r0, kc, xs);
+    } else if (tier == 1) {
+      decode_body<1, BF, MODE, NT, 4>(a, e, jb, active, cc, row_slot + r0, kc, xs);
+    } else {
+      decode_body<0, BF, MODE, NT, 2>(a, e, jb, active, cc, row_slot + r0, kc, xs);
+    }
+    __syncthreads();  // the next pass restages the same LDS rows
   }
 }
 
 template <int MODE, int NT>
-int launch_decode_nt(bool bf, const DecodeArgs& a, int64_t grid, hipStream_t s) {
+int launch_decode_nt(bool bf, const DecodeArgs& a, int kc, size_t lds, int64_t grid,
+                     hipStream_t s) {
   if (bf)
-    hipLaunchKernelGGL((moe_decode_kernel<true, MODE, NT>), dim3((unsigned)grid), dim3(DNT), 0, s,
-                       a);
+    hipLaunchKernelGGL((moe_decode_kernel<true, MODE, NT>), dim3((unsigned)grid), dim3(DNT),
+                       lds, s, a, kc);
   else
-    hipLaunchKernelGGL((moe_decode_kernel<false, MODE, NT>), dim3((unsigned)grid), dim3(DNT), 0,
-                       s, a);
+    hipLaunchKernelGGL((moe_decode_kernel<false, MODE, NT>), dim3((unsigned)grid), dim3(DNT),
+                       lds, s, a, kc);
   return check_launch("moe_decode_kernel");
 }
 
@@ -469,14 +512,22 @@ int launch_decode(bool bf, int mode, const void* ids, int ids_dtype, int T, int 
   const int64_t units = max_active * ((n_blocks + DW - 1) / DW);
   const int64_t grid = 8 * cdiv(units, 8);
   if (grid == 0) return EXQ_SUCCESS;
+  // Staged rows: the most tokens any expert can hold; the contraction is
+  // staged in chunks of kc elements so the rows fit the LDS budget.
+  const int nt = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+  const int rows = T * k < nt * 16 ? T * k : nt * 16;
+  int kc = (int)((X_LDS_BUDGET / (rows * 2) - 8) / 128 * 128);
+  if (kc > K) kc = K;
+  if (kc < 128) kc = 128;
+  const size_t lds = (size_t)rows * (kc + 8) * 2;
   if (mode == D_GATEUP) {
-    if (T <= 16) return launch_decode_nt<D_GATEUP, 1>(bf, a, grid, s);
-    if (T <= 32) return launch_decode_nt<D_GATEUP, 2>(bf, a, grid, s);
-    return launch_decode_nt<D_GATEUP, 4>(bf, a, grid, s);
+    if (nt == 1) return launch_decode_nt<D_GATEUP, 1>(bf, a, kc, lds, grid, s);
+    if (nt == 2) return launch_decode_nt<D_GATEUP, 2>(bf, a, kc, lds, grid, s);
+    return launch_decode_nt<D_GATEUP, 4>(bf, a, kc, lds, grid, s);
   }
-  if (T <= 16) return launch_decode_nt<D_DOWN, 1>(bf, a, grid, s);
-  if (T <= 32) return launch_decode_nt<D_DOWN, 2>(bf, a, grid, s);
-  return launch_decode_nt<D_DOWN, 4>(bf, a, grid, s);
+  if (nt == 1) return launch_decode_nt<D_DOWN, 1>(bf, a, kc, lds, grid, s);
+  if (nt == 2) return launch_decode_nt<D_DOWN, 2>(bf, a, kc, lds, grid, s);
+  return launch_decode_nt<D_DOWN, 4>(bf, a, kc, lds, grid, s);
 }
 
 }  // namespace exq

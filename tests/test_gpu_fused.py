@@ -203,3 +203,21 @@ def test_moe_grouped_gemm_unquantised(dtype, device):
     Wm[2] = 0
     ref = moe.grouped_gemm_sorted(a, Wm, r_ends)
     assert_close_rel(out, ref, TOL, f"grouped gemm {dtype}")
+
+
+@pytest.mark.parametrize("T", [4, 40, 100])
+def test_fused_duplicate_ids_randint_routing(T, device):
+    """torch.randint routing (the reference benches' convention) can repeat an
+    expert inside one token's top-k; every (token, k) slot still counts."""
+    from exq_amd.kernels import fused_experts
+    banner(f"fused duplicate ids T={T}")
+    cfg = SMALL
+    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, 31, device)
+    rng = np.random.default_rng(T)
+    ids = rng.integers(0, cfg.n_experts, size=(T, 8))
+    w = rng.random((T, 8)).astype(np.float32)
+    x = _hidden(T, cfg.hidden, 8, device)
+    out = fused_experts(x, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                        torch.from_numpy(ids).to(device))
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, f"duplicate ids T={T}")
