@@ -32,16 +32,51 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{ROOT / 'include'}",
     f"-I{CSRC}",
+    # per-kernel register / scratch report, checked below
+    "-Rpass-analysis=kernel-resource-usage",
 ]
+
+
+def _resource_report(text: str) -> dict:
+    """{kernel: {"scratch": bytes/lane, "vgprs": n, "agprs": n, "occupancy": waves/SIMD}}"""
+    out, cur = {}, None
+    for line in text.splitlines():
+        if "remark:" not in line:
+            continue
+        body = line.split("remark:", 1)[1].strip()
+        body = body.replace("[-Rpass-analysis=kernel-resource-usage]", "").strip()
+        if body.startswith("Function Name:"):
+            cur = body.split(":", 1)[1].strip()
+            out[cur] = {}
+        elif cur is not None and ":" in body:
+            key, val = body.rsplit(":", 1)
+            key = key.strip()
+            val = val.strip()
+            if key.startswith("ScratchSize"):
+                out[cur]["scratch"] = int(val)
+            elif key == "VGPRs":
+                out[cur]["vgprs"] = int(val)
+            elif key == "AGPRs":
+                out[cur]["agprs"] = int(val)
+            elif key.startswith("Occupancy"):
+                out[cur]["occupancy"] = int(val)
+    return out
 
 
 def _compile(src: Path, obj: Path) -> str:
     cmd = [HIPCC, *CFLAGS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)
+    text = r.stdout + r.stderr
+    err = "\n".join(l for l in text.splitlines()
+                    if noise not in l and "kernel-resource-usage" not in l
+                    and not l.lstrip().startswith(("|", "^")) and not l[:6].strip().isdigit())
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+    # A kernel that spills to scratch streams its spills through HBM: refuse it.
+    spilled = {k: v for k, v in _resource_report(text).items() if v.get("scratch", 0) > 0}
+    if spilled:
+        raise RuntimeError(f"{src.name}: kernels use scratch memory: {spilled}")
     return err
 
 

@@ -151,7 +151,7 @@ constexpr int X_LDS_BUDGET = 72 * 1024;
 // kc_alloc + 8 halfs); INT4 experts get the (0,4,1,5,2,6,3,7) order that
 // matches the nibble expansion.
 template <int MODE>
-__device__ __noinline__ void stage_rows(const DecodeArgs& a, const int* row_slot, int nrows,
+__device__ __forceinline__ void stage_rows(const DecodeArgs& a, const int* row_slot, int nrows,
                                         int k0, int kc, int xstride, bool int4_order,
                                         uint16_t* xs) {
   const int ppr = kc >> 3;  // 16-byte pieces per row
