@@ -68,14 +68,23 @@ __device__ __forceinline__ f32x4_t dmfma(const uint4& a, const uint4& b, f32x4_t
   }
 }
 
-template <bool BF>
-__device__ __forceinline__ uint4 ddeq4(uint32_t p) {
-  constexpr uint32_t M = BF ? 0x43004300u : 0x64006400u;
+// (a & m) | c in one VALU op.  gfx9 VOP3 encodings take no literal
+// constants, so the compiler splits the expression into AND + OR; with the
+// constants held in VGPRs v_and_or_b32 does it in one.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+
+// 8 packed nibbles (k offsets 0..7) -> 8 exact 16-bit floats (base + nibble)
+// in k order (0,4,1,5,2,6,3,7); mask = 0x000F000F, magic = base exponent bits.
+__device__ __forceinline__ uint4 ddeq4(uint32_t p, uint32_t mask, uint32_t magic) {
   uint4 o;
-  o.x = (p & 0x000F000Fu) | M;
-  o.y = ((p >> 4) & 0x000F000Fu) | M;
-  o.z = ((p >> 8) & 0x000F000Fu) | M;
-  o.w = ((p >> 12) & 0x000F000Fu) | M;
+  o.x = and_or(p, mask, magic);
+  o.y = and_or(p >> 4, mask, magic);
+  o.z = and_or(p >> 8, mask, magic);
+  o.w = and_or(p >> 12, mask, magic);
   return o;
 }
 
@@ -144,52 +153,52 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// LDS budget for the staged activation rows of one work-group.
-constexpr int X_LDS_BUDGET = 72 * 1024;
+// Staged activation rows per work-group: rows * kc <= X_ELEMS halfs.
+constexpr int X_ELEMS = 32768;
 
-// Stage activation rows [0, nrows) x k in [k0, k0 + kc) into LDS (row stride
-// kc_alloc + 8 halfs); INT4 experts get the (0,4,1,5,2,6,3,7) order that
-// matches the nibble expansion.
+typedef const void __attribute__((address_space(1)))* gptr_t;
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+// Stage activation rows [0, nrows) x k in [k0, k0 + kcc) into LDS with
+// global_load_lds_dwordx4: each wave instruction moves 64 16-byte pieces to 64
+// consecutive LDS slots (lane i -> base + 16 i), so no registers are used and
+// the copy overlaps nothing else in the wave.  Row m's piece q sits at slot
+// m * ppr + (q ^ (m & 15)): the XOR swizzle spreads the 16 rows that one
+// MFMA A-operand read touches over distinct banks.  Returns once this wave's
+// copies have landed; the caller synchronises the work-group.
 template <int MODE>
-__device__ __forceinline__ void stage_rows(const DecodeArgs& a, const int* row_slot, int nrows,
-                                        int k0, int kc, int xstride, bool int4_order,
-                                        uint16_t* xs) {
-  const int ppr = kc >> 3;  // 16-byte pieces per row
+__device__ __forceinline__ void stage_rows_lds(const DecodeArgs& a, const int* row_slot,
+                                               int nrows, int k0, int kcc, int ppr,
+                                               uint4* xs) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int total = nrows * ppr;
-  for (int base = threadIdx.x; base < total; base += DNT * 4) {
-    uint4 v[4];
-    int dst[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int pidx = base + u * DNT;
-      dst[u] = -1;
-      if (pidx < total) {
-        const int m = pidx / ppr;
-        const int q = pidx - m * ppr;
-        const int slot = row_slot[m];
-        const int64_t row = MODE == D_GATEUP ? (int64_t)(slot / a.kp) : (int64_t)slot;
-        v[u] = *reinterpret_cast<const uint4*>(a.x + row * a.x_stride + k0 + q * 8);
-        dst[u] = m * xstride + q * 8;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      if (dst[u] >= 0)
-        *reinterpret_cast<uint4*>(xs + dst[u]) = int4_order ? dperm(v[u]) : v[u];
+  const int pcc = kcc >> 3;
+  for (int pb = wave * 64; pb < total; pb += DNT) {
+    const int p = pb + lane;
+    const int m = p / ppr;
+    const int qs = p - m * ppr;
+    if (p < total && qs < pcc) {
+      const int q = qs ^ (m & 15);
+      const int slot = row_slot[m];
+      const int64_t row = MODE == D_GATEUP ? (int64_t)(slot / a.kp) : (int64_t)slot;
+      __builtin_amdgcn_global_load_lds((gptr_t)(a.x + row * a.x_stride + k0 + q * 8),
+                                       (lptr_t)(xs + pb), 16, 0, 0);
     }
   }
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this wave's copies have landed
 }
 
 template <int TIER, bool BF, int MODE, int NT, int P>
 __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, bool active,
-                                            int cnt, const int* row_slot, int kc,
-                                            uint16_t* xs) {
+                                            int cnt, const int* row_slot, int kc, int gshift,
+                                            uint4* xs) {
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15, kq = lane >> 4;
-  const int ntiles = (cnt + 15) >> 4;
+  const int ntiles = NT == 1 ? 1 : (cnt + 15) >> 4;
   const int nkb = a.K >> 7;
-  const int kcb = kc >> 7;            // k-blocks per staged chunk
-  const int xstride = kc + 8;         // halfs per staged row
+  const int kcb = kc >> 7;            // k-blocks per staged chunk (power of two if < nkb)
+  const bool chunked = kc < a.K;
+  const int ppr = kc >> 3;            // 16-byte pieces per staged row
 
   int rows[2];
   if (MODE == D_GATEUP) {
@@ -204,14 +213,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
   const unsigned char* rp[2] = {nullptr, nullptr};
   const uint16_t* sp[2] = {nullptr, nullptr};
   float rowscale[2] = {1.f, 1.f};
-  const int ngs = TIER == 2 ? a.K / a.group_size : 1;
   if (active) {
 #pragma unroll
     for (int rs = 0; rs < 2; ++rs) {
       const int64_t r = ebase + rows[rs];
       if constexpr (TIER == 2) {
         rp[rs] = a.w.i4 + r * (a.K / 2) + kq * 16;
-        sp[rs] = a.w.i4_scales + r * ngs;
+        sp[rs] = a.w.i4_scales + r * (a.K / a.group_size);
       } else if constexpr (TIER == 1) {
         rp[rs] = reinterpret_cast<const unsigned char*>(a.w.i8) + r * a.K + kq * 32;
         rowscale[rs] = f16_bits_to_f32(a.w.i8_scales[r]);
@@ -231,10 +239,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
       const uint4* src = reinterpret_cast<const uint4*>(rp[rs] + (int64_t)kb * KBSTRIDE);
 #pragma unroll
       for (int h = 0; h < QPK; ++h) wq[slotp][rs][h] = src[h];
-      if constexpr (TIER == 2) wsc[slotp][rs] = sp[rs][(kb * 128) / a.group_size];
+      if constexpr (TIER == 2) wsc[slotp][rs] = sp[rs][kb >> gshift];
     }
   };
-  // Weight stream first: its HBM latency overlaps the activation staging.
+
+  // Activations land in LDS before the weight stream is issued (vector-memory
+  // results return in issue order, so staging behind the weights would wait
+  // for them).
+  stage_rows_lds<MODE>(a, row_slot, cnt, 0, kc < a.K ? kc : a.K, ppr, xs);
+  __syncthreads();
   if (active) {
 #pragma unroll
     for (int p = 0; p < P; ++p)
@@ -248,12 +261,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
     tot1[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const uint4 negb = neg_base_operand<TIER, BF>();
-  // A-operand rows beyond cnt read row cnt-1: finite values whose outputs are dropped.
-  int arow[NT];
+  uint32_t dq_mask = 0x000F000Fu, dq_magic = BF ? 0x43004300u : 0x64006400u;
+  // A-operand rows beyond cnt read row cnt-1: finite values whose outputs are
+  // dropped.  arow = first slot of the row, aswz = its XOR swizzle.
+  int arow[NT], aswz[NT];
 #pragma unroll
   for (int tt = 0; tt < NT; ++tt) {
     const int q = tt * 16 + r16;
-    arow[tt] = (q < cnt ? q : cnt - 1) * xstride + kq * 32;
+    const int row = q < cnt ? q : cnt - 1;
+    arow[tt] = row * ppr;
+    aswz[tt] = row & 15;
   }
 
   for (int kb0 = 0; kb0 < nkb; kb0 += P) {
@@ -261,11 +278,11 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
     for (int p = 0; p < P; ++p) {
       const int kb = kb0 + p;
       if (kb < nkb) {
-        if (kb % kcb == 0) {  // next staged chunk (uniform across the work-group)
-          if (kb > 0) __syncthreads();
+        if (chunked && kb > 0 && (kb & (kcb - 1)) == 0) {  // next chunk (uniform)
+          __syncthreads();
           const int k0 = kb * 128;
           const int kcc = a.K - k0 < kc ? a.K - k0 : kc;
-          stage_rows<MODE>(a, row_slot, cnt, k0, kcc, xstride, TIER == 2, xs);
+          stage_rows_lds<MODE>(a, row_slot, cnt, k0, kcc, ppr, xs);
           __syncthreads();
         }
         if (active) {
@@ -275,10 +292,10 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
           for (int rs = 0; rs < 2; ++rs) {
             if constexpr (TIER == 2) {
               const uint4 w = wq[p][rs][0];
-              bfr[rs][0] = ddeq4<BF>(w.x);
-              bfr[rs][1] = ddeq4<BF>(w.y);
-              bfr[rs][2] = ddeq4<BF>(w.z);
-              bfr[rs][3] = ddeq4<BF>(w.w);
+              bfr[rs][0] = ddeq4(w.x, dq_mask, dq_magic);
+              bfr[rs][1] = ddeq4(w.y, dq_mask, dq_magic);
+              bfr[rs][2] = ddeq4(w.z, dq_mask, dq_magic);
+              bfr[rs][3] = ddeq4(w.w, dq_mask, dq_magic);
               sc[rs] = f16_bits_to_f32(wsc[p][rs]);
             } else if constexpr (TIER == 1) {
               const uint4 w0 = wq[p][rs][0], w1 = wq[p][rs][1];
@@ -296,14 +313,16 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
             }
           }
           if (kb + P < nkb) load_w(p, kb + P);  // refill this ring slot
-          const int koff = (kb % kcb) * 128;
+          const int kpiece = (chunked ? (kb & (kcb - 1)) : kb) * 16 + kq * 4;
 #pragma unroll
           for (int tt = 0; tt < NT; ++tt) {
             if (tt < ntiles) {
               uint4 xa[4];
 #pragma unroll
-              for (int d = 0; d < 4; ++d)
-                xa[d] = *reinterpret_cast<const uint4*>(xs + arow[tt] + koff + d * 8);
+              for (int d = 0; d < 4; ++d) {
+                xa[d] = xs[arow[tt] + ((kpiece + d) ^ aswz[tt])];
+                if constexpr (TIER == 2) xa[d] = dperm(xa[d]);
+              }
               f32x4_t init = {0.f, 0.f, 0.f, 0.f};
               if constexpr (TIER != 0) {
 #pragma unroll
@@ -354,8 +373,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a, int e, int jb, 
   }
 }
 
-template <bool BF, int MODE, int NT>
-__global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a, int kc) {
+template <bool BF, int MODE, int NT, bool MIXED>
+__global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a, int kc, int gshift) {
   extern __shared__ uint4 dyn_lds[];
   __shared__ uint32_t bitmap[DW][MAX_BM_WORDS];
   __shared__ int row_slot[64 * MAX_ID_REGS];
@@ -414,78 +433,83 @@ __global__ void __launch_bounds__(DNT) moe_decode_kernel(DecodeArgs a, int kc) {
   for (int t = 0; t < q0; ++t) wbits &= wbits - 1u;
   const int e = wl * 32 + (__ffs(wbits) - 1);
 
-  // 5. the expert's slots in ascending order (extended slot t*kp + j)
+  // 5. the expert's slots in ascending order (extended slot t*kp + j), as a
+  //    table in LDS.  A token routed twice to one expert (repeated ids) adds
+  //    rows; cnt <= T*k <= 1024.
   int cnt;
-  uint64_t m[MAX_ID_REGS];
   if (e < a.E) {
-    cnt = 0;
+    uint64_t m[MAX_ID_REGS];
+    int pre[MAX_ID_REGS + 1];
+    pre[0] = 0;
 #pragma unroll
     for (int i = 0; i < MAX_ID_REGS; ++i) {
       m[i] = __ballot(idr[i] == e);
-      cnt += __popcll(m[i]);
+      pre[i + 1] = pre[i] + __popcll(m[i]);
+    }
+    cnt = pre[MAX_ID_REGS];
+    for (int r = threadIdx.x; r < cnt; r += DNT) {
+      int i = 0;
+#pragma unroll
+      for (int j = 1; j < MAX_ID_REGS; ++j) i = (r >= pre[j]) ? j : i;
+      uint64_t mi = m[0];
+      int pi = 0;
+#pragma unroll
+      for (int j = 1; j < MAX_ID_REGS; ++j) {
+        if (j == i) {
+          mi = m[j];
+          pi = pre[j];
+        }
+      }
+      const int s = 64 * i + nth_set_bit(mi, r - pi);
+      const int t = s / a.k;
+      row_slot[r] = t * a.kp + (s - t * a.k);
     }
   } else {
     cnt = a.T;
-  }
-  // Slot table in LDS.  A token routed twice to one expert (duplicate ids)
-  // simply adds rows; cnt <= T*k <= 1024.
-  if (wave == 0) {
-    for (int r0 = 0; r0 < cnt; r0 += 64) {
-      int r = r0 + lane;
-      if (r < cnt) {
-        int slot;
-        if (e < a.E) {
-          int s = 0;
-#pragma unroll
-          for (int i = 0; i < MAX_ID_REGS; ++i) {
-            const int ci = __popcll(m[i]);
-            if (r >= 0 && r < ci) s = 64 * i + nth_set_bit(m[i], r);
-            r -= ci;
-          }
-          const int t = s / a.k;
-          slot = t * a.kp + (s - t * a.k);
-        } else {
-          slot = r * a.kp + a.k + (e - a.E);
-        }
-        row_slot[r0 + lane] = slot;
-      }
-    }
+    for (int r = threadIdx.x; r < cnt; r += DNT) row_slot[r] = r * a.kp + a.k + (e - a.E);
   }
   __syncthreads();
 
-  uint16_t* xs = reinterpret_cast<uint16_t*>(dyn_lds);
-  const int tier = a.w.tier ? (int)a.w.tier[e] : 2;
+  uint4* xs = dyn_lds;
+  const int tier = MIXED ? (int)a.w.tier[e] : 2;
   // Rows are processed 16*NT at a time (one pass unless ids repeat).
   for (int r0 = 0; r0 < cnt; r0 += NT * 16) {
     const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
-    if (tier == 2) {
-      decode_body<2, BF, MODE, NT, 8>(a, e, jb, active, cc, row_slot + r0, kc, xs);
+    // Every tier streams 256 bytes per lane per ring (8 / 4 / 2 k-blocks).
+    if (!MIXED || tier == 2) {
+      decode_body<2, BF, MODE, NT, 8>(a, e, jb, active, cc, row_slot + r0, kc, gshift, xs);
     } else if (tier == 1) {
-      decode_body<1, BF, MODE, NT, 4>(a, e, jb, active, cc, row_slot + r0, kc, xs);
+      decode_body<1, BF, MODE, NT, 4>(a, e, jb, active, cc, row_slot + r0, kc, gshift, xs);
     } else {
-      decode_body<0, BF, MODE, NT, 2>(a, e, jb, active, cc, row_slot + r0, kc, xs);
+      decode_body<0, BF, MODE, NT, 2>(a, e, jb, active, cc, row_slot + r0, kc, gshift, xs);
     }
     __syncthreads();  // the next pass restages the same LDS rows
   }
 }
 
 template <int MODE, int NT>
-int launch_decode_nt(bool bf, const DecodeArgs& a, int kc, size_t lds, int64_t grid,
-                     hipStream_t s) {
-  if (bf)
-    hipLaunchKernelGGL((moe_decode_kernel<true, MODE, NT>), dim3((unsigned)grid), dim3(DNT),
-                       lds, s, a, kc);
+int launch_decode_nt(bool bf, const DecodeArgs& a, int kc, int gshift, size_t lds,
+                     int64_t grid, hipStream_t s) {
+  const dim3 g((unsigned)grid), b(DNT);
+  const bool mixed = a.w.tier != nullptr;
+  if (bf && mixed)
+    hipLaunchKernelGGL((moe_decode_kernel<true, MODE, NT, true>), g, b, lds, s, a, kc, gshift);
+  else if (bf)
+    hipLaunchKernelGGL((moe_decode_kernel<true, MODE, NT, false>), g, b, lds, s, a, kc, gshift);
+  else if (mixed)
+    hipLaunchKernelGGL((moe_decode_kernel<false, MODE, NT, true>), g, b, lds, s, a, kc, gshift);
   else
-    hipLaunchKernelGGL((moe_decode_kernel<false, MODE, NT>), dim3((unsigned)grid), dim3(DNT),
-                       lds, s, a, kc);
+    hipLaunchKernelGGL((moe_decode_kernel<false, MODE, NT, false>), g, b, lds, s, a, kc, gshift);
   return check_launch("moe_decode_kernel");
 }
 
 }  // namespace
 
-bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared) {
+bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared,
+                           int64_t group_size) {
+  const int64_t gkb = group_size / 128;  // k-blocks per scale group: a power of two
   return T >= 1 && T <= 64 && T * k <= 64 * MAX_ID_REGS && Ep <= 32 * MAX_BM_WORDS &&
-         n_shared <= 64;
+         n_shared <= 64 && gkb >= 1 && (gkb & (gkb - 1)) == 0;
 }
 
 int launch_decode(bool bf, int mode, const void* ids, int ids_dtype, int T, int k, int kp,
@@ -512,22 +536,28 @@ int launch_decode(bool bf, int mode, const void* ids, int ids_dtype, int T, int 
   const int64_t units = max_active * ((n_blocks + DW - 1) / DW);
   const int64_t grid = 8 * cdiv(units, 8);
   if (grid == 0) return EXQ_SUCCESS;
-  // Staged rows: the most tokens any expert can hold; the contraction is
-  // staged in chunks of kc elements so the rows fit the LDS budget.
+  // Staged rows: the most rows one pass can hold; the contraction is staged
+  // in power-of-two chunks of kc elements so rows * kc <= X_ELEMS.
   const int nt = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
   const int rows = T * k < nt * 16 ? T * k : nt * 16;
-  int kc = (int)((X_LDS_BUDGET / (rows * 2) - 8) / 128 * 128);
-  if (kc > K) kc = K;
-  if (kc < 128) kc = 128;
-  const size_t lds = (size_t)rows * (kc + 8) * 2;
-  if (mode == D_GATEUP) {
-    if (nt == 1) return launch_decode_nt<D_GATEUP, 1>(bf, a, kc, lds, grid, s);
-    if (nt == 2) return launch_decode_nt<D_GATEUP, 2>(bf, a, kc, lds, grid, s);
-    return launch_decode_nt<D_GATEUP, 4>(bf, a, kc, lds, grid, s);
+  int kc = K;
+  if ((int64_t)rows * K > X_ELEMS) {
+    kc = 128;
+    while ((int64_t)rows * kc * 2 <= X_ELEMS) kc *= 2;
   }
-  if (nt == 1) return launch_decode_nt<D_DOWN, 1>(bf, a, kc, lds, grid, s);
-  if (nt == 2) return launch_decode_nt<D_DOWN, 2>(bf, a, kc, lds, grid, s);
-  return launch_decode_nt<D_DOWN, 4>(bf, a, kc, lds, grid, s);
+  const size_t lds = (size_t)rows * kc * 2;
+  int gshift = 0;
+  if (group_size > 0) {
+    while ((128 << gshift) < group_size) ++gshift;
+  }
+  if (mode == D_GATEUP) {
+    if (nt == 1) return launch_decode_nt<D_GATEUP, 1>(bf, a, kc, gshift, lds, grid, s);
+    if (nt == 2) return launch_decode_nt<D_GATEUP, 2>(bf, a, kc, gshift, lds, grid, s);
+    return launch_decode_nt<D_GATEUP, 4>(bf, a, kc, gshift, lds, grid, s);
+  }
+  if (nt == 1) return launch_decode_nt<D_DOWN, 1>(bf, a, kc, gshift, lds, grid, s);
+  if (nt == 2) return launch_decode_nt<D_DOWN, 2>(bf, a, kc, gshift, lds, grid, s);
+  return launch_decode_nt<D_DOWN, 4>(bf, a, kc, gshift, lds, grid, s);
 }
 
 }  // namespace exq

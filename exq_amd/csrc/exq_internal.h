@@ -55,7 +55,8 @@ int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, 
 // Self-routing decode kernels (decode.hip).  mode 0: gate/up + SiLU into mid
 // rows indexed by slot t*kp + j; mode 1: down projection into fp32 partial
 // rows indexed the same way.
-bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared);
+bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared,
+                           int64_t group_size);
 int launch_decode(bool bf, int mode, const void* ids, int ids_dtype, int T, int k, int kp,
                   int E, int Ep, const uint16_t* x, int64_t x_stride, int K,
                   const int8_t* tier, const int32_t* index, const uint16_t* bf16,

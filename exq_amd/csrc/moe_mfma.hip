@@ -564,7 +564,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   struct HookReset {  // the hook is consumed by this call, whatever happens
     ~HookReset() { g_stage_events_set = false; }
   } hook_reset;
-  const bool decode = decode_path_supported(T, k, Ep, p->n_shared);
+  const bool decode = decode_path_supported(T, k, Ep, p->n_shared, p->group_size);
   int st = record_stage(0, s);
   if (st) return st;
   // The decode path routes inside its GEMM waves; the routing plan runs only
