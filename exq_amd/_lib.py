@@ -136,14 +136,17 @@ def require_gpu(*tensors: torch.Tensor) -> torch.device:
     return dev
 
 
-# Per-(device, stream) workspace cache: reused across calls on one stream,
-# which is safe because launches on one stream are ordered.
-_ws_cache: dict[tuple[int, int], torch.Tensor] = {}
+# Per-(device, stream, kind) workspace cache: reused across calls on one
+# stream, which is safe because launches on one stream are ordered.  The
+# fused-layer workspace ("fused") is kept apart from the scratch of the other
+# entry points: its first bytes hold counters that must stay zero between
+# calls, and the fused kernels leave them zero.
+_ws_cache: dict[tuple[int, int, str], torch.Tensor] = {}
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, nbytes: int, kind: str = "scratch") -> torch.Tensor:
     key = (device.index if device.index is not None else torch.cuda.current_device(),
-           stream_handle(device))
+           stream_handle(device), kind)
     buf = _ws_cache.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(nbytes, 1 << 20)
@@ -156,4 +159,3 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 def clear_workspace_cache() -> None:
     _ws_cache.clear()
-

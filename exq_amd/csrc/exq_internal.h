@@ -52,16 +52,42 @@ int launch_route_plan(const RoutePlanParams& p, hipStream_t stream);
 int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, int tier,
                         int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream);
 
-// Self-routing decode kernels (decode.hip).  mode 0: gate/up + SiLU into mid
-// rows indexed by slot t*kp + j; mode 1: down projection into fp32 partial
-// rows indexed the same way.
-bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared,
+// One-launch decode layer (decode.hip): routing, gate/up + SiLU, down and the
+// combine in a single persistent kernel.  `sync` points at the zero-filled
+// counter region (kDecodeSyncBytes at the start of the fused workspace).
+constexpr int kDecodeMaxBuckets = 1024;   // routed + shared experts
+constexpr int kDecodeMaxHBlocks = 512;    // H / 64
+constexpr size_t kDecodeSyncBytes = (size_t)(kDecodeMaxBuckets + kDecodeMaxHBlocks + 2) * 128;
+
+struct DecodeLaunch {
+  const void* ids;
+  int ids_dtype;
+  const void* topk_w;
+  int w_dtype;
+  int T, k, kp, E, Ep;
+  const uint16_t* x;
+  const uint16_t* w13_bf16;
+  const int8_t* w13_i8;
+  const uint16_t* w13_i8_scales;
+  const uint8_t* w13_i4;
+  const uint16_t* w13_i4_scales;
+  const uint16_t* w2_bf16;
+  const int8_t* w2_i8;
+  const uint16_t* w2_i8_scales;
+  const uint8_t* w2_i4;
+  const uint16_t* w2_i4_scales;
+  const int8_t* tier;      // [Ep] or null (all INT4)
+  const int32_t* index;    // [Ep] or null
+  int H, I, group_size;
+  uint16_t* mid;           // [T * kp, I]
+  float* part;             // [T * kp, H]
+  uint16_t* out;           // [T, H]
+  int* sync;
+  bool bf;
+};
+
+bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, int64_t H,
                            int64_t group_size);
-int launch_decode(bool bf, int mode, const void* ids, int ids_dtype, int T, int k, int kp,
-                  int E, int Ep, const uint16_t* x, int64_t x_stride, int K,
-                  const int8_t* tier, const int32_t* index, const uint16_t* bf16,
-                  const int8_t* i8, const uint16_t* i8_scales, const uint8_t* i4,
-                  const uint16_t* i4_scales, int n_rows, int inter, int group_size, void* out,
-                  int64_t out_stride, int n_blocks, hipStream_t s);
+int launch_decode_layer(const DecodeLaunch& d, hipStream_t s);
 
 }  // namespace exq

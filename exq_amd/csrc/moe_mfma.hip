@@ -474,10 +474,13 @@ int record_stage(int i, hipStream_t s) {
 
 // ---- workspace layout of the fused forward --------------------------------------
 struct FusedLayout {
-  size_t hdr, ends, sorted, tg, mid, partial, total;
+  size_t sync, hdr, ends, sorted, tg, mid, partial, total;
   int64_t n, tg_cap;
 };
 
+// The decode counters sit at offset 0 with a fixed size, so every fused call
+// finds them at the same place whatever its problem size; each decode launch
+// leaves them zero again.
 FusedLayout fused_layout(const exq_moe_problem& p) {
   FusedLayout L;
   const int64_t kp = p.top_k + p.n_shared;
@@ -485,6 +488,7 @@ FusedLayout fused_layout(const exq_moe_problem& p) {
   L.n = p.n_tokens * kp;
   L.tg_cap = tg_capacity(L.n, Ep);
   size_t off = 0;
+  L.sync = off;     off = align_up(off + kDecodeSyncBytes, 256);
   L.hdr = off;      off = align_up(off + 64, 256);
   L.ends = off;     off = align_up(off + (size_t)(Ep + 1) * 4, 256);
   L.sorted = off;   off = align_up(off + (size_t)L.n * 4, 256);
@@ -564,11 +568,12 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   struct HookReset {  // the hook is consumed by this call, whatever happens
     ~HookReset() { g_stage_events_set = false; }
   } hook_reset;
-  const bool decode = decode_path_supported(T, k, Ep, p->n_shared, p->group_size);
+  const bool decode =
+      decode_path_supported(T, k, Ep, p->n_shared, p->hidden_size, p->group_size);
   int st = record_stage(0, s);
   if (st) return st;
-  // The decode path routes inside its GEMM waves; the routing plan runs only
-  // when the caller asked for the routing arrays.
+  // The decode path routes inside its persistent kernel; the routing plan
+  // runs only when the caller asked for the routing arrays.
   if (!decode || sort_order_out || expert_ends_out) {
     st = launch_route_plan(rp, s);
     if (st) return st;
@@ -577,18 +582,30 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   if (st) return st;
 
   if (decode) {
-    st = launch_decode(bf, 0, topk_ids, p->ids_dtype, T, k, kp, E, Ep,
-                       reinterpret_cast<const uint16_t*>(hidden), H, H, b13.tier, b13.index,
-                       b13.bf16, b13.i8, b13.i8_scales, b13.i4, b13.i4_scales, 2 * I, I,
-                       (int)p->group_size, ws + L.mid, I, I / 16, s);
+    DecodeLaunch d{};
+    d.ids = topk_ids;
+    d.ids_dtype = p->ids_dtype;
+    d.topk_w = topk_weights;
+    d.w_dtype = p->weights_dtype;
+    d.T = T; d.k = k; d.kp = kp; d.E = E; d.Ep = Ep;
+    d.x = reinterpret_cast<const uint16_t*>(hidden);
+    d.w13_bf16 = b13.bf16; d.w13_i8 = b13.i8; d.w13_i8_scales = b13.i8_scales;
+    d.w13_i4 = b13.i4; d.w13_i4_scales = b13.i4_scales;
+    d.w2_bf16 = b2.bf16; d.w2_i8 = b2.i8; d.w2_i8_scales = b2.i8_scales;
+    d.w2_i4 = b2.i4; d.w2_i4_scales = b2.i4_scales;
+    d.tier = b13.tier;
+    d.index = b13.index;
+    d.H = H; d.I = I; d.group_size = (int)p->group_size;
+    d.mid = reinterpret_cast<uint16_t*>(ws + L.mid);
+    d.part = reinterpret_cast<float*>(ws + L.partial);
+    d.out = reinterpret_cast<uint16_t*>(out);
+    d.sync = reinterpret_cast<int*>(ws + L.sync);
+    d.bf = bf;
+    st = launch_decode_layer(d, s);
     if (st) return st;
     st = record_stage(2, s);
     if (st) return st;
-    st = launch_decode(bf, 1, topk_ids, p->ids_dtype, T, k, kp, E, Ep,
-                       reinterpret_cast<const uint16_t*>(ws + L.mid), I, I, b2.tier, b2.index,
-                       b2.bf16, b2.i8, b2.i8_scales, b2.i4, b2.i4_scales, H, I,
-                       (int)p->group_size, ws + L.partial, H, H / 32, s);
-    if (st) return st;
+    return record_stage(3, s);
   } else {
     GemmArgs g{};
     g.hdr = rp.hdr;

@@ -61,7 +61,9 @@ def fused_experts(hidden_states: torch.Tensor, w13_packed: torch.Tensor,
     [0, E) are dropped).  Returns [T, H] in the activation dtype.  The call is
     stream-ordered and never synchronises with the host.  ``workspace`` (uint8,
     at least ``moe_workspace_bytes(...)``) replaces the per-stream cached one,
-    e.g. for HIP-graph capture.
+    e.g. for HIP-graph capture; it must be zero-filled when first used
+    (``torch.zeros``) and must not be shared with other entry points: its first
+    bytes hold counters that every call leaves zero.
     """
     if activation != "silu":
         raise ValueError(f"unsupported activation {activation!r} (only 'silu')")
@@ -83,7 +85,7 @@ def fused_experts(hidden_states: torch.Tensor, w13_packed: torch.Tensor,
     p = _problem(hidden_states, topk_ids, topk_weights, E, I, gs)
     L = _lib.lib()
     need = L.exq_moe_workspace_size(p)
-    ws = workspace if workspace is not None else _lib.workspace(dev, need)
+    ws = workspace if workspace is not None else _lib.workspace(dev, need, "fused")
     _lib.check(L.exq_moe_int4_fused_forward(
         p, hidden_states.data_ptr(), topk_ids.data_ptr(), topk_weights.data_ptr(),
         w13_packed.data_ptr(), w13_scales.data_ptr(), w2_packed.data_ptr(),
@@ -250,7 +252,8 @@ def fused_experts_mixed(hidden_states: torch.Tensor, bank: MixedExpertBank,
     p = _problem(hidden_states, topk_ids, topk_weights, bank.n_experts, bank.inter_size,
                  bank.group_size, bank.n_shared)
     L = _lib.lib()
-    ws = workspace if workspace is not None else _lib.workspace(dev, L.exq_moe_workspace_size(p))
+    ws = workspace if workspace is not None else _lib.workspace(
+        dev, L.exq_moe_workspace_size(p), "fused")
     cb = bank.c_bank()
     _lib.check(L.exq_moe_mixed_forward(
         p, hidden_states.data_ptr(), topk_ids.data_ptr(), topk_weights.data_ptr(), cb,

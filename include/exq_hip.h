@@ -224,12 +224,21 @@ typedef struct exq_expert_bank {
   const uint16_t* int4_w2_scales;   /* [n4, H, I/g]    */
 } exq_expert_bank;
 
-/* Workspace bytes needed by the fused entry points for this problem. */
+/*
+ * Workspace bytes needed by the fused entry points for this problem.  The
+ * first bytes of a fused-layer workspace hold synchronisation counters of the
+ * one-launch decode kernel (T <= 64): the workspace must be zero-filled
+ * before its first use, every call leaves those counters zero again, and a
+ * workspace must not be shared by calls that may run concurrently or with
+ * other entry points.
+ */
 size_t exq_moe_workspace_size(const exq_moe_problem* problem);
 
 /*
  * The whole INT4 MoE layer: routing preparation, gate/up INT4 GEMM fused with
- * SiLU-and-mul, down INT4 GEMM, top-k weighted combine.  Replaces the
+ * SiLU-and-mul, down INT4 GEMM, top-k weighted combine.  Decode batches
+ * (T <= 64) run as one persistent kernel; larger batches as routing plan +
+ * two grouped MFMA GEMMs + combine.  Replaces the
  * pipeline of _exq_forward_cuda (exq/runtime/sglang_backend.py:65-158:
  * moe_align_block_size -> build_ends_from_slots -> gather_hidden -> GEMM1 ->
  * silu_and_mul -> GEMM2 -> combine) and moe_int4_full_forward
