@@ -10,12 +10,21 @@ steps); inputs are resident in HBM before the timed region.
 
 Printed: one JSON line with µs per MoE layer (value), tokens/s, the achieved
 HBM bandwidth on activated-expert weight bytes, the roofline of the dominant
-kernel (gate/up INT4 GEMM + SiLU, timed with HIP events on its stream), the
-decode-batch sweep (1, 4, 16, 64) and the reference's CPU path timed on this
-host.
+kernel (the gate/up INT4 GEMM + SiLU decode kernel, timed with HIP events
+recorded on its stream around it), the decode-batch sweep (1, 4, 16, 64) and
+the reference's CPU path timed on this host.
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--batch 16]
                     [--sweep 1,4,16,64] [--layers 48] [--no-cpu]
+
+Counter runs (HBM traffic of the dominant kernel, rocprofv3 --pmc):
+
+    rocprofv3 --pmc FETCH_SIZE --output-format csv -d DIR -o fetch -- \
+        python3 bench.py --pmc-run
+    python3 bench.py --pmc-summary DIR/.../fetch_counter_collection.csv
+
+--pmc-run first copies a 256 MiB buffer (the calibration: a plain copy of
+known size) and then runs the 48 layers once at the bench batch, eagerly.
 """
 from __future__ import annotations
 
@@ -45,7 +54,43 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--cpu-reps", type=int, default=10)
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="calibration copy + one eager pass, for rocprofv3 --pmc")
+    ap.add_argument("--pmc-summary", type=str, default="",
+                    help="per-kernel mean of a rocprofv3 counter CSV")
     return ap.parse_args()
+
+
+CALIB_BYTES = 256 << 20
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "qwen3_t16_gateup_pmc.md")
+
+
+def pmc_summary(path):
+    """Mean counter value per (kernel, counter) of a rocprofv3 counter CSV."""
+    import csv
+    from collections import defaultdict
+    acc = defaultdict(list)
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name") or row.get("Kernel-Name") or ""
+            ctr = row.get("Counter_Name") or row.get("Counter-Name") or ""
+            val = row.get("Counter_Value") or row.get("Counter-Value") or "nan"
+            acc[(name, ctr)].append(float(val))
+    for (name, ctr), v in sorted(acc.items(), key=lambda kv: -sum(kv[1])):
+        print(f"{len(v):6d}  {ctr:12s} mean {sum(v) / len(v):14.1f}  {name[:110]}")
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the gate/up decode kernel from the committed
+    counter summary (a line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except (OSError, ValueError):
+        return None
+    return None
 
 
 def log(msg):
@@ -137,8 +182,10 @@ def time_steps(stack, b, steps, warmup, use_graph):
 
 
 def stage_times(stack, b, reps=3):
-    """Per-kernel durations (µs) from HIP events recorded around each kernel
-    of every layer call on the call's stream (eager launches)."""
+    """Per-kernel durations (µs) of every layer call (eager launches): the
+    decode kernels are launched with hipExtLaunchKernelGGL start / stop
+    events on the call's stream, so events 0 -> 1 time the gate/up kernel and
+    2 -> 3 the down kernel exactly."""
     import torch
     from exq_amd import _lib
     L = _lib.lib()
@@ -158,12 +205,11 @@ def stage_times(stack, b, reps=3):
             fused_experts(b.x, p13, s13, p2, s2, b.wts[l], b.ids[l], out=b.out, workspace=b.ws)
             i += 1
     torch.cuda.synchronize()
-    route = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
-    gateup = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
+    gateup = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
     down = [e[2].elapsed_time(e[3]) * 1e3 for e in evs]
+    layer = [e[0].elapsed_time(e[3]) * 1e3 for e in evs]
     mean = lambda v: sum(v) / len(v)  # noqa: E731
-    return {"route_us": mean(route), "gateup_us": mean(gateup), "down_us": mean(down),
-            "layer_us": mean([r + g + d for r, g, d in zip(route, gateup, down)])}
+    return {"gateup_us": mean(gateup), "down_us": mean(down), "layer_us": mean(layer)}
 
 
 def cpu_baseline(stack, b, reps):
@@ -203,6 +249,9 @@ def main():
               f"WORLD_SIZE={world}); the expert-parallel sharding is design-only, see "
               "DESIGN.md", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     import torch
     from exq_amd import synth
     if not torch.cuda.is_available():
@@ -210,6 +259,13 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     cfg = synth.CONFIGS["qwen3"]
+    if args.pmc_run:
+        src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy: {CALIB_BYTES} bytes read, {CALIB_BYTES} written")
+        del src, dst
     t0 = time.time()
     stack = Stack(cfg, args.layers, dev)
     log(f"packed {args.layers} layers in {time.time() - t0:.1f}s "
@@ -217,6 +273,12 @@ def main():
     use_graph = not args.no_graph
 
     b = Batch(stack, args.batch, dev)
+    if args.pmc_run:
+        run_step(stack, b)
+        torch.cuda.synchronize()
+        log(f"one eager pass of {args.layers} layers at T={args.batch}; activated experts "
+            f"per layer {sum(b.active) / len(b.active):.2f}")
+        return
     ms, wall = time_steps(stack, b, args.steps, args.warmup, use_graph)
     us_layer = ms * 1e3 / args.layers
     gbps = b.bytes / (ms * 1e-3) / 1e9
@@ -224,12 +286,13 @@ def main():
         f"(host wall {wall:.3f} ms/step)")
     st = stage_times(stack, b)
     log(f"stage events: {st}")
-    # Dominant kernel: the one-launch decode layer kernel (events 1 -> 2 bracket
-    # it on the call's stream); its algorithmic bytes are the activated
-    # experts' weights + scales of both projections.
+    # Dominant kernel: the gate/up decode kernel (events 0 -> 1 time it on the
+    # call's stream); its algorithmic bytes are the activated experts'
+    # gate/up weights + fp16 scales (2I*H/2 + 2I*(H/128)*2 bytes per expert).
     kern_us = st["gateup_us"]
-    kern_bytes = b.bytes / len(b.active)
+    kern_bytes = stack.w13_bytes * sum(b.active) / len(b.active)
     kern_gbps = kern_bytes / (kern_us * 1e-6) / 1e9
+    traffic = traffic_from_profile()
 
     sweep = []
     for T in [int(v) for v in args.sweep.split(",") if v.strip()]:
@@ -272,9 +335,10 @@ def main():
         "tokens_per_s": round(args.batch / (us_layer * 1e-6)),
         "achieved_GBps": round(gbps, 1),
         "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-        "roofline": {"bound": "hbm", "kernel": "moe_layer_kernel<bf16, NT=1> (whole decode layer)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "moe_decode_kernel<bf16, gate/up, NT=1, INT4 LDS path>",
                      "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": round(kern_bytes), "launch_us": round(kern_us, 3)},
         "stages_us": {k: round(v, 3) for k, v in st.items()},
         "sweep": sweep,

@@ -1,58 +1,74 @@
-// decode.hip -- the whole MoE layer in one launch for decode batches (T <= 64).
+// decode.hip -- the MoE layer for decode batches (T <= 64) in two launches.
 //
-// Persistent work-groups.  Every wave reads the (<= 1024) routed ids into
-// registers, marks the active experts in an LDS bitmap and counts them; the
-// work-group then loops over units
+//   gate/up kernel: unit = (active expert, 16 gate rows + the 16 matching up
+//                   rows); SiLU(gate) * up -> `mid` rows.
+//   down kernel:    unit = (active expert, ROWS_B output rows); fp32 partial
+//                   rows per routed slot; the last unit to finish a column
+//                   block of H combines it over each token's slots in fixed
+//                   order (deterministic) and writes `out`.
 //
-//   gate/up  (expert, 16 gate rows + the 16 matching up rows)     u <  NA
-//   down     (expert, 64 output rows)                             u >= NA
+// Both kernels route for themselves: every work-group reads the (<= 1024)
+// routed ids into LDS once, marks the active experts in a bitmap and counts
+// them; unit u belongs to the (u / nb)-th active expert (ascending id; routed
+// experts that received a slot, then the always-on shared experts).  The grid
+// is one resident round of work-groups (CUs x occupancy), each taking units
+// blockIdx.x, blockIdx.x + gridDim.x, ...  Each wave finds the expert's rows
+// itself with one ballot per 64 ids (ascending slot order -- the canonical
+// order of the reference's stable argsort), so no row table or barrier is
+// needed before the activation loads.
 //
-// taken round-robin (u = blockIdx.x, + gridDim.x, ...), all gate/up units
-// before any down unit.  The four waves of a work-group split the
-// contraction of a unit into contiguous k-block ranges, so many short weight
-// streams run at once and the tail of the launch stays short.
+// Per unit, the four waves split the contraction into contiguous k-block
+// ranges.  INT4 weights take the LDS path when a wave's range fits its 8 KB
+// region: the wave DMAs its whole slice with buffer_load ... lds, whole
+// 128-byte lines per row, into XOR-swizzled slots, so the slice is in flight
+// without occupying registers; measured, this streams better than 128-bit
+// register loads in the MFMA operand layout (16 rows x 64 B per instruction,
+// half lines).  Activation fragments (16-byte loads from L2) and the fp16
+// group scales stream through a 2-deep register ring.  Other cases (INT8 and
+// BF16 experts of a mixed bank, or a k-range too long for the region) stream
+// weights through a register ring instead.  Nibbles become exact bf16/f16
+// values (base + n) with one v_and_or_b32 per pair (the exponent-OR method of
+// Kim et al., "Who Says Elephants Can't Run", 2022) and feed
+// v_mfma_f32_16x16x32_{bf16,f16}; the constant base is removed by MFMAs of
+// the same activations against a -base operand; the fp16 group scale
+// multiplies each exact k-block sum in fp32.  The four waves' partial tiles
+// are summed through LDS.  INT4 weights pair k-offsets (0,4),(1,5),(2,6),
+// (3,7) inside each 8-group; the gate/up epilogue writes `mid` in that order
+// so the down kernel reads INT4 experts' rows without a permute.
 //
-// Dataflow instead of a kernel boundary: a down unit of expert e issues its
-// weight loads, then waits until all gate/up units of e have published their
-// `mid` rows (per-expert counter), then stages those rows.  Every down unit adds its fp32 partial rows for one 64-column
-// block of H and bumps that block's counter; the last unit to arrive sums the
-// block's partials over each token's k slots in fixed order (deterministic)
-// and writes the output.  Data shared between work-groups (mid rows, fp32
-// partials) is written and read with agent-coherent (sc1) accesses, and every
-// storing wave waits for its stores to complete before its work-group bumps a
-// counter, so no whole-cache writeback or invalidate is needed (on this part
-// agent-scope fences write back / invalidate the whole L2 of an XCD).  The
-// last combine zeroes the counters, so the sync
-// region is zero again when the launch ends.  Waits are bounded: a wait that
-// runs out sets an error word instead of hanging (the grid never exceeds the
-// number of co-resident work-groups, so waits end in practice).
-//
-// Per unit and wave: the weight stream goes through a register ring of P
-// k-blocks (one 128-bit load per lane per row set and k-block), issued before
-// the activation rows are staged into LDS with global_load_lds_dwordx4 (XOR
-// swizzled); weights and scales come through bounds-checked buffer loads.  Nibbles become exact bf16/f16 values (base + n) with one
-// v_and_or_b32 per pair (the exponent-OR method of Kim et al., "Who Says
-// Elephants Can't Run", 2022) and feed v_mfma_f32_16x16x32_{bf16,f16}; the
-// constant base is removed by MFMAs of the same activations against a -base
-// operand; the fp16 group scale multiplies each exact k-block sum in fp32.
-// The four waves' partial tiles are summed through LDS.
-#include <mutex>
-
+// The combine's fp32 partials are written and read with agent-coherent (sc1)
+// accesses; every storing wave waits for its stores before its work-group
+// bumps the column block's counter, so no whole-cache writeback or
+// invalidate is needed (on this part agent-scope fences write back /
+// invalidate the whole L2 of an XCD).  The last combine zeroes the counters,
+// so the sync region is zero again when the launch ends.
 #include "exq_internal.h"
+
+#include <hip/hip_ext.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
 
 namespace exq {
 namespace {
 
 constexpr int DW = 4;              // waves per work-group
 constexpr int DNT = DW * 64;
-constexpr int MAX_ID_REGS = 16;    // ids per lane: T * k <= 1024
+constexpr int MAX_SLOTS = 1024;    // T * (k + n_shared)
 constexpr int MAX_BM_WORDS = 32;   // active-expert bitmap: E + shared <= 1024
-constexpr int RING = 8;            // 128-bit weight registers per lane
-// Output rows of a down unit: 64 (four row sets), 32 when a pass holds
-// four 16-row tiles (register budget).
-__host__ __device__ constexpr int rows_b(int nt) { return nt == 4 ? 32 : 64; }
-constexpr int64_t SPIN_LIMIT = 1 << 22;
 constexpr int CPOL_SC1 = 16;       // cache-policy bits: sc1 (agent-coherent access)
+
+// Output rows of a down unit: 64 (four row sets), 32 when a pass holds two
+// or four 16-row tiles (register budget of the accumulators).
+__host__ __device__ constexpr int rows_b(int nt) { return nt == 1 ? 64 : 32; }
+
+// 128-bit registers per lane for the weight + activation ring.
+__host__ __device__ constexpr int ring_regs(int nt) { return nt == 1 ? 12 : 20; }
+
+// LDS bytes per wave: the INT4 weight slice of the DMA path and, after a
+// pass's k-loop, the wave's partial tiles.
+constexpr int WAVE_LDS = 8192;
 
 struct Proj {
   const uint16_t* bf16;
@@ -73,26 +89,21 @@ struct LayerArgs {
   const int8_t* tier;           // [Ep] or null (all INT4)
   const int32_t* index;         // [Ep] or null (identity)
   int H, I, gshift;             // group size = 128 << gshift
-  uint16_t* mid;                // [T * kp, I] activation dtype
+  uint16_t* mid;                // [T * kp, I] activation dtype, MFMA k-order
   float* part;                  // [T * kp, H] fp32
   uint16_t* out;                // [T, H]
-  int* sync;                    // counters, see sync_* below
+  int* sync;                    // combine counters, see sync_* below
   int nbA, nbB;                 // units per expert: I / 16, H / rows_b(NT)
-  int xw;                       // per-wave LDS staging budget (16-bit elements)
 };
 
 // Counter layout of the sync region (fixed, independent of the problem size):
 // one 128-byte line per counter.
 constexpr int SYNC_INTS = 32;
-__device__ __forceinline__ int* sync_a(const LayerArgs& a, int e) { return a.sync + e * SYNC_INTS; }
 __device__ __forceinline__ int* sync_c(const LayerArgs& a, int hb) {
   return a.sync + (kDecodeMaxBuckets + hb) * SYNC_INTS;
 }
 __device__ __forceinline__ int* sync_done(const LayerArgs& a) {
   return a.sync + (kDecodeMaxBuckets + kDecodeMaxHBlocks) * SYNC_INTS;
-}
-__device__ __forceinline__ int* sync_err(const LayerArgs& a) {
-  return a.sync + (kDecodeMaxBuckets + kDecodeMaxHBlocks + 1) * SYNC_INTS;
 }
 
 template <bool BF>
@@ -106,20 +117,16 @@ __device__ __forceinline__ f32x4_t dmfma(const uint4& a, const uint4& b, f32x4_t
   }
 }
 
-// (a & m) | c.  Plain C: gfx950 fuses it into one v_bitop3_b32 (or
-// v_and_or_b32), and the compiler's hazard tracking sees every instruction.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-  return (a & m) | c;
-}
-
 // 8 packed nibbles (k offsets 0..7) -> 8 exact 16-bit floats (base + nibble)
-// in k order (0,4,1,5,2,6,3,7); mask = 0x000F000F, magic = base exponent bits.
+// in k order (0,4,1,5,2,6,3,7).  `mask` (0x000F000F) is wave-uniform and
+// `magic` (the base's exponent bits) lives in a VGPR, so each pair is one
+// v_and_or_b32 plus a shift.
 __device__ __forceinline__ uint4 ddeq4(uint32_t p, uint32_t mask, uint32_t magic) {
   uint4 o;
-  o.x = and_or(p, mask, magic);
-  o.y = and_or(p >> 4, mask, magic);
-  o.z = and_or(p >> 8, mask, magic);
-  o.w = and_or(p >> 12, mask, magic);
+  o.x = (p & mask) | magic;
+  o.y = ((p >> 4) & mask) | magic;
+  o.z = ((p >> 8) & mask) | magic;
+  o.w = ((p >> 12) & mask) | magic;
   return o;
 }
 
@@ -140,7 +147,7 @@ __device__ __forceinline__ uint2 ddeq8(uint32_t p) {
   return o;
 }
 
-// Activation order used with INT4 weights: (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+// Natural k order (x0..x7) -> INT4 pairing order (x0,x4),(x1,x5),(x2,x6),(x3,x7).
 __device__ __forceinline__ uint4 dperm(const uint4& v) {
   uint4 o;
   o.x = (v.x & 0xffffu) | (v.z << 16);
@@ -149,6 +156,19 @@ __device__ __forceinline__ uint4 dperm(const uint4& v) {
   o.w = (v.y >> 16) | (v.w & 0xffff0000u);
   return o;
 }
+
+// Inverse of dperm: INT4 pairing order -> natural k order.
+__device__ __forceinline__ uint4 dperm_inv(const uint4& o) {
+  uint4 v;
+  v.x = (o.x & 0xffffu) | (o.y << 16);
+  v.y = (o.z & 0xffffu) | (o.w << 16);
+  v.z = (o.x >> 16) | (o.y & 0xffff0000u);
+  v.w = (o.z >> 16) | (o.w & 0xffff0000u);
+  return v;
+}
+
+// Position of natural k-offset j (0..7) of an 8-group in INT4 pairing order.
+__device__ __forceinline__ int pair_pos(int j) { return ((j & 3) << 1) | (j >> 2); }
 
 // Constant B operand holding -base in every element.
 template <int TIER, bool BF>
@@ -162,6 +182,83 @@ __device__ __forceinline__ uint4 neg_base_operand() {
 template <bool BF>
 __device__ __forceinline__ uint32_t to_act_bits(float v) {
   return BF ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+}
+
+// Wave-local waits written as volatile asm with a memory clobber, so the
+// compiler moves no memory access across them: LDS written by an LDS DMA
+// (global_load_lds) is only ordered by the vmcnt wait, which the compiler
+// does not model as a dependency of later LDS reads.
+__device__ __forceinline__ void wave_lds_fence() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS ops have completed
+}
+
+__device__ __forceinline__ void wait_vm_all() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads, stores and LDS DMA have landed
+}
+
+typedef void __attribute__((address_space(3)))* lptr_t;
+typedef const void __attribute__((address_space(1)))* gptr_t;
+
+// 16 bytes per lane from buffer `r` at byte offset `voff` into LDS at
+// lds + 16 * lane (buffer_load_dwordx4 ... lds); `lds` is wave-uniform.  The
+// builtin exists only for the device target.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)lds, 16, voff, 0, 0, 0);
+#endif
+}
+
+// Buffer resource over `bytes` bytes at `base` (gfx9 word 3): loads beyond
+// the range return zero instead of touching other memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+
+// The batch's routed ids and active-expert bitmap, per work-group.
+struct Route {
+  uint32_t bitmap[MAX_BM_WORDS];
+  int16_t ids[MAX_SLOTS];  // routed id of slot t*k + j (-1: dropped)
+};
+
+// Load the ids and build the bitmap (all threads); returns the number of
+// active experts and leaves this lane's bitmap word and prefix for
+// select_expert.
+__device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t& word, int& incl,
+                                     int& c) {
+  const int lane = threadIdx.x & 63;
+  const int n = a.T * a.k;
+  const int nw = (a.Ep + 31) >> 5;
+  if (threadIdx.x < MAX_BM_WORDS) r.bitmap[threadIdx.x] = 0u;
+  __syncthreads();
+  for (int s = threadIdx.x; s < n; s += DNT) {
+    const int64_t id = load_index(a.ids, a.ids_dtype, s);
+    const int v = (id >= 0 && id < a.E) ? (int)id : -1;
+    r.ids[s] = (int16_t)v;
+    if (v >= 0) atomicOr(&r.bitmap[v >> 5], 1u << (v & 31));
+  }
+  if (threadIdx.x < a.Ep - a.E && a.T > 0)
+    atomicOr(&r.bitmap[(a.E + threadIdx.x) >> 5], 1u << ((a.E + threadIdx.x) & 31));
+  __syncthreads();
+  word = lane < nw ? r.bitmap[lane] : 0u;
+  c = __popc(word);
+  // inclusive prefix of the per-word counts (< 64 each) from bit-sliced ballots
+  const uint64_t lt_or_eq = lane == 63 ? ~0ull : ((2ull << lane) - 1ull);
+  incl = 0;
+#pragma unroll
+  for (int b = 0; b < 6; ++b) incl += __popcll(__ballot((c >> b) & 1) & lt_or_eq) << b;
+  return __builtin_amdgcn_readlane(incl, 63);
+}
+
+// The ai-th active expert (ai < number of active experts).
+__device__ __forceinline__ int select_expert(int ai, uint32_t word, int incl, int c) {
+  const uint64_t hit = __ballot(incl - c <= ai && ai < incl);
+  const int wl = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)hit) - 1);
+  uint32_t wbits = __builtin_amdgcn_readlane(word, wl);
+  const int q0 = ai - (__builtin_amdgcn_readlane(incl, wl) - __builtin_amdgcn_readlane(c, wl));
+  for (int t = 0; t < q0; ++t) wbits &= wbits - 1u;
+  return wl * 32 + (__ffs(wbits) - 1);
 }
 
 // Index (0..63) of the q-th set bit of a 64-bit mask (q < popcount).
@@ -189,580 +286,649 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int q) {
   return base;
 }
 
-// Wave-local waits written as volatile asm with a memory clobber, so the
-// compiler moves no memory access across them: LDS written by an LDS DMA
-// (global_load_lds) is only ordered by the vmcnt wait, which the compiler
-// does not model as a dependency of later LDS reads.
-__device__ __forceinline__ void wave_lds_fence() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS ops have completed
-}
-
-__device__ __forceinline__ void wait_vm_all() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads and LDS DMA have landed
-}
-
-typedef void __attribute__((address_space(3)))* lptr_t;
-
-typedef const void __attribute__((address_space(1)))* gptr_t;
-
-// Buffer resource over `bytes` bytes at `base` (gfx9 word 3): loads beyond
-// the range return zero instead of touching other memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-
-// Stage activation rows [0, nrows) x k-blocks [kb0, kb0 + nkbc) into this
-// wave's LDS region with global_load_lds_dwordx4: each wave instruction moves
-// 64 16-byte pieces to 64 consecutive LDS slots, so no registers are used.
-// Row m's piece q sits at slot m * ppr + (q ^ (m & 15)): the XOR swizzle
-// spreads the 16 rows that one MFMA A-operand read touches over distinct
-// banks.  The caller waits (wait_vm_all) before reading.
-template <int PH>
-__device__ __forceinline__ void stage_rows(const LayerArgs& a, const int* row_slot, int nrows,
-                                           int kb0, int nkbc, int ppr, uint4* xs) {
-  const int lane = threadIdx.x & 63;
-  const int total = nrows * ppr;
-  const int pcc = nkbc * 16;
-  for (int pb = 0; pb < total; pb += 64) {
-    const int p = pb + lane;
-    const int m = p / ppr;
-    const int qs = p - m * ppr;
-    if (p < total && qs < pcc) {
-      const int q = qs ^ (m & 15);
-      const int slot = row_slot[m];
-      const uint16_t* src = PH == 0 ? a.x + (int64_t)(slot / a.kp) * a.H
-                                    : a.mid + (int64_t)slot * a.I;
-      __builtin_amdgcn_global_load_lds((gptr_t)(src + kb0 * 128 + q * 8), (lptr_t)(xs + pb), 16,
-                                       0, PH == 0 ? 0 : CPOL_SC1);
+// Expert e's rows (its routed slots t*kp + j in ascending order, the order of
+// the reference's stable sort; every token for a shared expert), found by
+// each wave on its own with one ballot per 64 ids: sl[tt] receives the slot
+// of row r0 + tt*16 + r16, or of the last row when that is beyond the count.
+// Returns the row count (wave-uniform).
+template <int NT>
+__device__ __forceinline__ int lane_slots(const LayerArgs& a, const Route& r, int e, int r0,
+                                          int (&sl)[NT]) {
+  const int lane = threadIdx.x & 63, r16 = lane & 15;
+  if (e >= a.E) {
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      const int q = r0 + tt * 16 + r16;
+      sl[tt] = (q < a.T ? q : a.T - 1) * a.kp + a.k + (e - a.E);
     }
+    return a.T;
+  }
+  const int n = a.T * a.k;
+  int cnt = 0, last = 0, found[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) found[tt] = -1;
+  for (int s0 = 0; s0 < n; s0 += 64) {
+    const int s = s0 + lane;
+    const uint64_t m = __ballot(s < n && r.ids[s] == e);
+    const int c = __popcll(m);
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) {
+      const int q = r0 + tt * 16 + r16;
+      if (found[tt] < 0 && q >= cnt && q < cnt + c) found[tt] = s0 + nth_set_bit(m, q - cnt);
+    }
+    if (c) last = s0 + 63 - __clzll(m);
+    cnt += c;
+  }
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    const int f = found[tt] < 0 ? last : found[tt];
+    const int t = f / a.k;
+    sl[tt] = t * a.kp + (f - t * a.k);
+  }
+  return cnt;
+}
+
+// Compile-time geometry of a (tier, phase, tiles-per-pass) instantiation.
+template <int TIER, int PH, int NT>
+struct Geo {
+  static constexpr int ROWS_B = rows_b(NT);
+  static constexpr int RS = PH == 0 ? 2 : ROWS_B / 16;              // row sets of 16 rows
+  static constexpr int QPK = TIER == 2 ? 1 : (TIER == 1 ? 2 : 4);   // uint4 per lane, k-block, row set
+  static constexpr int WSLOT = RS * QPK;                            // weight registers per k-block
+  static constexpr int SLOT = WSLOT + 4 * NT;                       // + activation fragments
+  static constexpr int P0 = ring_regs(NT) / SLOT;
+  static constexpr int P = P0 < 1 ? 1 : (P0 > 4 ? 4 : P0);          // ring depth (k-blocks)
+  static constexpr int KBSTRIDE = TIER == 2 ? 64 : (TIER == 1 ? 128 : 256);  // row bytes per k-block
+  static constexpr int CK = WAVE_LDS / (RS * 1024);                 // INT4 k-blocks a wave holds in LDS
+  static_assert(RS * NT * 1024 <= WAVE_LDS, "partial tiles exceed the wave's LDS region");
+};
+
+// Per-unit quantities shared by both k-loop variants.
+template <int TIER, int PH, int NT>
+struct UnitCtx {
+  using G = Geo<TIER, PH, NT>;
+  int lane, wave, r16, kq, K, nkb, lo, nmy, ng, rowbytes;
+  int64_t ebase;
+  __amdgpu_buffer_rsrc_t wr, wnull, sr, snull, xr, xnull, part_r;
+  float rowscale[G::RS];
+
+  __device__ __forceinline__ UnitCtx(const LayerArgs& a, int e, int blk) {
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    r16 = lane & 15;
+    kq = lane >> 4;
+    K = PH == 0 ? a.H : a.I;
+    nkb = K >> 7;
+    lo = (wave * nkb) >> 2;
+    nmy = (((wave + 1) * nkb) >> 2) - lo;  // k-blocks of this wave
+    const Proj& W = PH == 0 ? a.w13 : a.w2;
+    const int n_rows = PH == 0 ? 2 * a.I : a.H;
+    const int widx = a.index ? __builtin_amdgcn_readfirstlane(a.index[e]) : e;
+    ebase = (int64_t)widx * n_rows;
+    rowbytes = TIER == 2 ? K / 2 : (TIER == 1 ? K : 2 * K);
+    const unsigned char* wbase =
+        TIER == 2 ? W.i4
+                  : (TIER == 1 ? reinterpret_cast<const unsigned char*>(W.i8)
+                               : reinterpret_cast<const unsigned char*>(W.bf16));
+    wr = make_rsrc(wbase + ebase * rowbytes, (int64_t)n_rows * rowbytes);
+    wnull = make_rsrc(wbase + ebase * rowbytes, 0);
+    ng = nkb >> a.gshift;  // scale groups per row
+    const uint16_t* sbase = TIER == 2 ? W.i4_scales + ebase * ng : nullptr;
+    sr = make_rsrc(sbase, (int64_t)n_rows * ng * 2);
+    snull = make_rsrc(sbase, 0);
+    xr = PH == 0 ? make_rsrc(a.x, (int64_t)a.T * a.H * 2)
+                 : make_rsrc(a.mid, (int64_t)a.T * a.kp * a.I * 2);
+    xnull = make_rsrc(PH == 0 ? (const void*)a.x : (const void*)a.mid, 0);
+    part_r = make_rsrc(a.part, (int64_t)a.T * a.kp * a.H * 4);
+#pragma unroll
+    for (int rs = 0; rs < G::RS; ++rs) {
+      rowscale[rs] = 1.f;
+      if constexpr (TIER == 1) rowscale[rs] = f16_bits_to_f32(W.i8_scales[ebase + row(a, blk, rs * 16 + r16)]);
+    }
+  }
+  // Weight row of row-set row rr (0 <= rr < RS*16) of row block blk.
+  __device__ __forceinline__ int row(const LayerArgs& a, int blk, int rr) const {
+    return PH == 0 ? (rr < 16 ? 0 : a.I - 16) + blk * 16 + rr : blk * G::ROWS_B + rr;
+  }
+  // Byte offset of this lane's activation row (slot sl) in its tile.
+  __device__ __forceinline__ int xoff(const LayerArgs& a, int sl) const {
+    const int xrow = PH == 0 ? sl / a.kp : sl;
+    return (xrow * (PH == 0 ? a.H : a.I) + kq * 32) * 2;
+  }
+};
+
+// A operand of one 16-row tile (four 16x32 pieces) from its raw fragments,
+// and its -base sum (the exact correction for the +base in dequantised weights).
+// The gate/up phase reads activations in natural k order; `mid` is stored in
+// INT4 pairing order.
+template <int TIER, bool BF, int PH>
+__device__ __forceinline__ void make_a(const uint4* raw, uint4 (&xa)[4], f32x4_t& init) {
+  const uint4 negb = neg_base_operand<TIER, BF>();
+  init = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    xa[d] = raw[d];
+    if constexpr (PH == 0 && TIER == 2) xa[d] = dperm(xa[d]);
+    if constexpr (PH == 1 && TIER != 2) xa[d] = dperm_inv(xa[d]);
+  }
+  if constexpr (TIER != 0) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) init = dmfma<BF>(xa[d], negb, init);
   }
 }
 
-// Waits until *cnt >= target (agent scope), at most SPIN_LIMIT polls.
-__device__ void wait_counter(const LayerArgs& a, const int* cnt, int target) {
-  if ((threadIdx.x & 63) == 0) {
-    int64_t spins = 0;
-    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (++spins > SPIN_LIMIT) {
-        __hip_atomic_fetch_or(sync_err(a), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  wait_vm_all();
-}
-
-// One unit of work (phase PH: 0 gate/up + SiLU, 1 down + combine) for an
-// expert of precision tier TIER, in passes of NT*16 rows.
+// After a pass's k-loop: the four waves' partial tiles sit in their LDS
+// regions; sum them and write `mid` (gate/up: SiLU(gate) * up) or the fp32
+// partial rows (down).
 template <int TIER, bool BF, int PH, int NT>
-__device__ void unit_body(const LayerArgs& a, int e, int blk, int cnt, const int* row_slot,
-                          unsigned char* lds, int* s_flag, int n_active) {
-  constexpr int ROWS_B = rows_b(NT);
-  constexpr int RS = PH == 0 ? 2 : ROWS_B / 16;                 // row sets of 16 rows
-  constexpr int QPK = TIER == 2 ? 1 : (TIER == 1 ? 2 : 4);      // uint4 per lane, k-block, row set
-  constexpr int RING_NT = NT <= 2 ? RING : RING / 2;            // fewer ring registers at NT=4
-  constexpr int P0 = RING_NT / (RS * QPK);
-  constexpr int P = P0 > 0 ? P0 : 1;                            // ring depth (k-blocks)
-  constexpr int KBSTRIDE = TIER == 2 ? 64 : (TIER == 1 ? 128 : 256);  // row bytes per k-block
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r16 = lane & 15, kq = lane >> 4;
-  const int K = PH == 0 ? a.H : a.I;
-  const int nkb = K >> 7;
-  const int lo = (wave * nkb) >> 2;
-  const int nmy = (((wave + 1) * nkb) >> 2) - lo;  // k-blocks of this wave
-  const Proj& W = PH == 0 ? a.w13 : a.w2;
-  const int n_rows = PH == 0 ? 2 * a.I : a.H;
-  const int widx = a.index ? a.index[e] : e;
-  const int64_t ebase = (int64_t)widx * n_rows;
-
-  int rows[RS];
+__device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TIER, PH, NT>& u,
+                                            const unsigned char* lds, const int (&sl)[NT], int cc,
+                                            int ntiles, int blk) {
+  // slot of row tt*16 + 4*kq + i of the pass: held by lane 4*kq + i of tile tt
+  auto slot_of = [&](int tt, int i) {
+    int v = sl[0];
 #pragma unroll
-  for (int rs = 0; rs < RS; ++rs) {
-    if (PH == 0)
-      rows[rs] = (rs == 0 ? 0 : a.I) + blk * 16 + r16;
-    else
-      rows[rs] = blk * ROWS_B + rs * 16 + r16;
+    for (int j = 1; j < NT; ++j)
+      if (j == tt) v = sl[j];
+    return __shfl(v, u.kq * 4 + i, 64);
+  };
+  using G = Geo<TIER, PH, NT>;
+  constexpr int RS = G::RS, ROWS_B = G::ROWS_B;
+  auto red = [&](int w, int rs, int tt) {
+    return reinterpret_cast<const float4*>(lds + w * WAVE_LDS)[(rs * NT + tt) * 64 + u.lane];
+  };
+  // lane (r16, kq) of tile tt holds rows tt*16 + 4*kq + i, column r16
+  if constexpr (PH == 0) {
+    const int tt = u.wave;
+    if (tt < ntiles) {
+      float g[4] = {0.f, 0.f, 0.f, 0.f}, v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < DW; ++w) {
+        const float4 pg = red(w, 0, tt);
+        const float4 pu = red(w, 1, tt);
+        g[0] += pg.x; g[1] += pg.y; g[2] += pg.z; g[3] += pg.w;
+        v[0] += pu.x; v[1] += pu.y; v[2] += pu.z; v[3] += pu.w;
+      }
+      const int col = blk * 16 + (u.r16 & 8) + pair_pos(u.r16 & 7);  // INT4 pairing order
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = tt * 16 + u.kq * 4 + i;
+        const int slot = slot_of(tt, i);
+        if (q < cc) {
+          const float y = silu_f32(g[i] * u.rowscale[0]) * (v[i] * u.rowscale[1]);
+          a.mid[(int64_t)slot * a.I + col] = (uint16_t)to_act_bits<BF>(y);
+        }
+      }
+    }
+  } else {
+    bool stored = false;
+    for (int it = threadIdx.x; it < RS * ntiles * 64; it += DNT) {
+      const int rtl = it >> 6;
+      const int rs = rtl / ntiles, tt = rtl - rs * ntiles;
+      float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < DW; ++w) {
+        const float4 pv = red(w, rs, tt);
+        s[0] += pv.x; s[1] += pv.y; s[2] += pv.z; s[3] += pv.w;
+      }
+      float rsc = 1.f;
+#pragma unroll
+      for (int j = 0; j < RS; ++j)
+        if (j == rs) rsc = u.rowscale[j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int q = tt * 16 + u.kq * 4 + i;
+        const int slot = slot_of(tt, i);
+        if (q < cc)
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __builtin_bit_cast(uint32_t, s[i] * rsc), u.part_r,
+              (slot * a.H + blk * ROWS_B + rs * 16 + u.r16) * 4, 0, CPOL_SC1);
+      }
+      stored = true;
+    }
+    if (stored) wait_vm_all();  // this wave's partial rows have completed
   }
-  // This expert's weights (and INT4 scales) behind bounds-checked buffer
-  // resources; each lane keeps a 32-bit offset per row set.
-  const int rowbytes = TIER == 2 ? K / 2 : (TIER == 1 ? K : 2 * K);
-  const unsigned char* wbase =
-      TIER == 2 ? W.i4
-                : (TIER == 1 ? reinterpret_cast<const unsigned char*>(W.i8)
-                             : reinterpret_cast<const unsigned char*>(W.bf16));
-  const __amdgpu_buffer_rsrc_t wr =
-      make_rsrc(wbase + ebase * rowbytes, (int64_t)n_rows * rowbytes);
-  const int ng = nkb >> a.gshift;  // scale groups per row
-  const __amdgpu_buffer_rsrc_t sr =
-      make_rsrc(TIER == 2 ? W.i4_scales + ebase * ng : nullptr, (int64_t)n_rows * ng * 2);
-  int voff[RS], soff[RS];
-  float rowscale[RS];
-#pragma unroll
-  for (int rs = 0; rs < RS; ++rs) {
-    voff[rs] = rows[rs] * rowbytes + kq * 16 * QPK;
-    soff[rs] = rows[rs] * ng * 2;
-    rowscale[rs] = 1.f;
-    if constexpr (TIER == 1) rowscale[rs] = f16_bits_to_f32(W.i8_scales[ebase + rows[rs]]);
-  }
+}
 
-  uint4 wq[P][RS][QPK];
-  uint32_t wsc[P][RS];
-  auto load_w = [&](int slotp, int kb) {
+// Down phase, after the unit's last pass: count the unit in for its column
+// block; the last of the block's n_active units combines the block.
+template <bool BF, int ROWS_B>
+__device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Route& rt, int blk,
+                                                    int n_active, int* s_flag) {
+  if (threadIdx.x == 0) {
+    const int old =
+        __hip_atomic_fetch_add(sync_c(a, blk), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = old == n_active - 1;
+  }
+  __syncthreads();
+  if (!*s_flag) return;
+  // out[t, h..h+3] = sum over the token's slots j (ascending) of weight *
+  // partial; a chunk of eight slots' loads is issued at once
+  const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, (int64_t)a.T * a.kp * a.H * 4);
+  const __amdgpu_buffer_rsrc_t part_null = make_rsrc(a.part, 0);
+  const int h0 = blk * ROWS_B;
+  for (int idx = threadIdx.x; idx < a.T * (ROWS_B / 4); idx += DNT) {
+    const int t = idx / (ROWS_B / 4);
+    const int h = h0 + (idx - t * (ROWS_B / 4)) * 4;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < a.kp; j0 += 8) {
+      float4 pv[8];
+      float wg[8];
 #pragma unroll
-    for (int rs = 0; rs < RS; ++rs) {
+      for (int jj = 0; jj < 8; ++jj) {
+        const int j = j0 + jj;
+        bool ok = j < a.kp;
+        float wgt = 1.f;
+        if (ok && j < a.k) {
+          ok = rt.ids[t * a.k + j] >= 0;
+          if (ok) wgt = load_as_f32(a.topk_w, a.w_dtype, (int64_t)t * a.k + j);
+        }
+        wg[jj] = ok ? wgt : 0.f;
+        pv[jj] = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(
+                        ok ? part_r : part_null, ok ? ((t * a.kp + j) * a.H + h) * 4 : 0, 0,
+                        CPOL_SC1));
+      }
 #pragma unroll
-      for (int h = 0; h < QPK; ++h)
-        wq[slotp][rs][h] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff[rs] + h * 16, kb * KBSTRIDE, 0));
-      if constexpr (TIER == 2)
-        wsc[slotp][rs] = __builtin_amdgcn_raw_buffer_load_b16(sr, soff[rs], (kb >> a.gshift) * 2, 0);
+      for (int jj = 0; jj < 8; ++jj) {
+        if (j0 + jj < a.kp) {
+          acc[0] += wg[jj] * pv[jj].x;
+          acc[1] += wg[jj] * pv[jj].y;
+          acc[2] += wg[jj] * pv[jj].z;
+          acc[3] += wg[jj] * pv[jj].w;
+        }
+      }
+    }
+    uint2 o;
+    o.x = to_act_bits<BF>(acc[0]) | (to_act_bits<BF>(acc[1]) << 16);
+    o.y = to_act_bits<BF>(acc[2]) | (to_act_bits<BF>(acc[3]) << 16);
+    *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.H + h) = o;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(sync_c(a, blk), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int d = __hip_atomic_fetch_add(sync_done(a), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == a.nbB - 1)  // every block is combined
+      __hip_atomic_store(sync_done(a), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// INT4 unit whose k-blocks fit the wave's LDS region (nmy <= CK): every
+// wave DMAs its whole weight slice (RS*16 rows x nmy k-blocks) into LDS with
+// buffer_load ... lds.  Each DMA instruction moves 64 16-byte pieces; a row's
+// pieces are contiguous in memory (whole 128-byte lines whenever nmy >= 2)
+// and land at slot rr*4*nmy + (c ^ (rr & xm)), an XOR swizzle that makes the
+// MFMA-layout reads (16 rows, same column) conflict-free.  No registers hold
+// the weights in flight, so a work-group's whole slice is requested at once.
+// Activation fragments (and the fp16 group scales) stream through a 2-deep
+// register ring.
+template <bool BF, int PH, int NT>
+__device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt, int e, int blk,
+                                             unsigned char* lds) {
+  using G = Geo<2, PH, NT>;
+  constexpr int RS = G::RS, CK = G::CK;
+  constexpr int DA = NT == 4 ? 1 : 2;  // activation k-blocks in flight
+  const UnitCtx<2, PH, NT> u(a, e, blk);
+  unsigned char* region = lds + u.wave * WAVE_LDS;
+  const int p4 = 4 * u.nmy;                 // 16-byte pieces per row in LDS
+  const int xm = (u.nmy & 1) ? 3 : 7;       // swizzle mask keeps c ^ (rr & xm) < p4
+  auto dma = [&]() {
+    for (int j = 0; j < RS * u.nmy; ++j) {  // 64 pieces per instruction
+      const int p = j * 64 + u.lane;
+      const int rr = p / p4;
+      const int c = (p - rr * p4) ^ (rr & xm);
+      dma16(u.wr, region + j * 1024, u.row(a, blk, rr) * u.rowbytes + u.lo * 64 + c * 16);
     }
   };
+  auto wslot = [&](int kbl, int rs) {  // LDS byte offset of this lane's piece
+    const int rr = rs * 16 + u.r16;
+    const int c = kbl * 4 + u.kq;
+    return kbl < u.nmy ? (rr * p4 + (c ^ (rr & xm))) * 16 : 0;
+  };
 
-  uint4* xs = reinterpret_cast<uint4*>(lds + (size_t)wave * a.xw * 2);
-  const __amdgpu_buffer_rsrc_t mid_r = make_rsrc(a.mid, (int64_t)a.T * a.kp * a.I * 2);
-  const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, (int64_t)a.T * a.kp * a.H * 4);
-  const uint4 negb = neg_base_operand<TIER, BF>();
-  const uint32_t dq_mask = 0x000F000Fu, dq_magic = BF ? 0x43004300u : 0x64006400u;
+  dma();
+  int sl[NT];
+  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, 0, sl));
+
+  const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(dq_magic));  // keep the magic in a VGPR: one v_and_or_b32 per pair
+  int soff[RS];
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) soff[rs] = u.row(a, blk, rs * 16 + u.r16) * u.ng * 2;
 
   for (int r0 = 0; r0 < cnt; r0 += NT * 16) {
     const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
     const int ntiles = (cc + 15) >> 4;
-    const int* rsl = row_slot + r0;
-    // k-blocks per staged chunk: a power of two covering this wave's range
-    // when the rows fit, else the most that fit (restaged chunk by chunk)
-    int kcb = 1;
-    while (kcb < nmy && cc * (kcb * 2) * 128 <= a.xw) kcb *= 2;
-    const int ppr = kcb * 16;  // 16-byte pieces per staged row
-
-    // 1. weights first: they do not depend on anything
+    if (r0 > 0) {  // the partial tiles of the previous pass overwrote the slice
+      dma();
+      lane_slots<NT>(a, rt, e, r0, sl);
+    }
+    int xo[NT];
 #pragma unroll
-    for (int p = 0; p < P; ++p)
-      if (p < nmy) load_w(p, lo + p);
-    // 2. a down unit needs every gate/up unit of its expert
-    if (PH == 1 && r0 == 0) wait_counter(a, sync_a(a, e), a.nbA);
-    // 3. activation rows of the first chunk
-    if (nmy > 0) stage_rows<PH>(a, rsl, cc, lo, nmy < kcb ? nmy : kcb, ppr, xs);
-    wait_vm_all();
+    for (int tt = 0; tt < NT; ++tt) xo[tt] = u.xoff(a, sl[tt]);
+    uint4 areg[DA][4 * NT];
+    uint32_t sreg[DA][RS];
+    auto load_a = [&](int p, int kbl) {  // zeros past the wave's range
+      const bool ok = kbl < u.nmy;
+      const int kb = ok ? u.lo + kbl : u.lo;
+#pragma unroll
+      for (int rs = 0; rs < RS; ++rs)
+        sreg[p][rs] = __builtin_amdgcn_raw_buffer_load_b16(ok ? u.sr : u.snull, soff[rs],
+                                                           (kb >> a.gshift) * 2, 0);
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          areg[p][tt * 4 + d] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(ok ? u.xr : u.xnull, xo[tt] + d * 16,
+                                                           kb * 256, 0));
+    };
+#pragma unroll
+    for (int p = 0; p < DA; ++p) load_a(p, p);
+    wait_vm_all();  // the weight slice has landed in LDS
 
     f32x4_t tot[RS][NT];
 #pragma unroll
     for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
       for (int t = 0; t < NT; ++t) tot[rs][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    // A-operand rows beyond cc read row cc-1: finite values whose outputs are dropped.
-    int arow[NT], aswz[NT];
 #pragma unroll
-    for (int tt = 0; tt < NT; ++tt) {
-      const int q = tt * 16 + r16;
-      const int row = q < cc ? q : cc - 1;
-      arow[tt] = row * ppr;
-      aswz[tt] = row & 15;
-    }
-
-    for (int kb0 = 0; kb0 < nmy; kb0 += P) {
+    for (int kbl = 0; kbl < CK; ++kbl) {
+      const int p = kbl % DA;
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        const int kbl = kb0 + p;  // k-block index within this wave's range
-        if (kbl < nmy) {
-          if (kbl > 0 && (kbl & (kcb - 1)) == 0) {  // next staged chunk (wave-local)
-            wave_lds_fence();
-            const int rem = nmy - kbl;
-            stage_rows<PH>(a, rsl, cc, lo + kbl, rem < kcb ? rem : kcb, ppr, xs);
-            wait_vm_all();
+      for (int tt = 0; tt < NT; ++tt) {
+        if (tt < ntiles) {
+          uint4 xa[4];
+          f32x4_t init;
+          make_a<2, BF, PH>(&areg[p][tt * 4], xa, init);
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs) {
+            const uint4 w = *reinterpret_cast<const uint4*>(region + wslot(kbl, rs));
+            f32x4_t acc = dmfma<BF>(xa[0], ddeq4(w.x, dq_mask, dq_magic), init);
+            acc = dmfma<BF>(xa[1], ddeq4(w.y, dq_mask, dq_magic), acc);
+            acc = dmfma<BF>(xa[2], ddeq4(w.z, dq_mask, dq_magic), acc);
+            acc = dmfma<BF>(xa[3], ddeq4(w.w, dq_mask, dq_magic), acc);
+            tot[rs][tt] += f16_bits_to_f32(sreg[p][rs]) * acc;
           }
-          const int kpiece = (kbl & (kcb - 1)) * 16 + kq * 4;
-          // One row set's weights as MFMA B operands (exact base + q values).
-          auto dequant = [&](int rs, uint4 (&bfr)[4], float& sc) {
-            sc = 1.f;
-            if constexpr (TIER == 2) {
-              const uint4 w = wq[p][rs][0];
-              bfr[0] = ddeq4(w.x, dq_mask, dq_magic);
-              bfr[1] = ddeq4(w.y, dq_mask, dq_magic);
-              bfr[2] = ddeq4(w.z, dq_mask, dq_magic);
-              bfr[3] = ddeq4(w.w, dq_mask, dq_magic);
-              sc = f16_bits_to_f32(wsc[p][rs]);
-            } else if constexpr (TIER == 1) {
-              const uint4 w0 = wq[p][rs][0], w1 = wq[p][rs][1];
-              const uint2 d0 = ddeq8<BF>(w0.x), d1 = ddeq8<BF>(w0.y);
-              const uint2 d2 = ddeq8<BF>(w0.z), d3 = ddeq8<BF>(w0.w);
-              const uint2 d4 = ddeq8<BF>(w1.x), d5 = ddeq8<BF>(w1.y);
-              const uint2 d6 = ddeq8<BF>(w1.z), d7 = ddeq8<BF>(w1.w);
-              bfr[0] = uint4{d0.x, d0.y, d1.x, d1.y};
-              bfr[1] = uint4{d2.x, d2.y, d3.x, d3.y};
-              bfr[2] = uint4{d4.x, d4.y, d5.x, d5.y};
-              bfr[3] = uint4{d6.x, d6.y, d7.x, d7.y};
-            } else {
-#pragma unroll
-              for (int h = 0; h < 4; ++h) bfr[h] = wq[p][rs][h];
-            }
-          };
-          // A operand of tile tt (four 16x32 pieces) and its -base sum.
-          auto load_a = [&](int tt, uint4 (&xa)[4], f32x4_t& init) {
-            init = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              xa[d] = xs[arow[tt] + ((kpiece + d) ^ aswz[tt])];
-              if constexpr (TIER == 2) xa[d] = dperm(xa[d]);
-            }
-            if constexpr (TIER != 0) {
-#pragma unroll
-              for (int d = 0; d < 4; ++d) init = dmfma<BF>(xa[d], negb, init);
-            }
-          };
-          if constexpr (NT <= 2) {
-            // A operands of every tile first, then one row set at a time
-            uint4 xa[NT][4];
-            f32x4_t init[NT];
-#pragma unroll
-            for (int tt = 0; tt < NT; ++tt)
-              if (tt < ntiles) load_a(tt, xa[tt], init[tt]);
-#pragma unroll
-            for (int rs = 0; rs < RS; ++rs) {
-              uint4 bfr[4];
-              float sc;
-              dequant(rs, bfr, sc);
-#pragma unroll
-              for (int tt = 0; tt < NT; ++tt) {
-                if (tt < ntiles) {
-                  f32x4_t acc = init[tt];
-#pragma unroll
-                  for (int d = 0; d < 4; ++d) acc = dmfma<BF>(xa[tt][d], bfr[d], acc);
-                  tot[rs][tt] += sc * acc;
-                }
-              }
-            }
-          } else {
-            // four tiles: one tile's A operand at a time (fewer live registers)
-#pragma unroll
-            for (int tt = 0; tt < NT; ++tt) {
-              if (tt < ntiles) {
-                uint4 xa[4];
-                f32x4_t init;
-                load_a(tt, xa, init);
-#pragma unroll
-                for (int rs = 0; rs < RS; ++rs) {
-                  uint4 bfr[4];
-                  float sc;
-                  dequant(rs, bfr, sc);
-                  f32x4_t acc = init;
-#pragma unroll
-                  for (int d = 0; d < 4; ++d) acc = dmfma<BF>(xa[d], bfr[d], acc);
-                  tot[rs][tt] += sc * acc;
-                }
-              }
-            }
-          }
-          if (kbl + P < nmy) load_w(p, lo + kbl + P);  // refill this ring slot
         }
       }
+      load_a(p, kbl + DA);
     }
-
-    // 4. sum the four waves' partial tiles through LDS (aliases the staging area)
-    __syncthreads();
-    float4* red = reinterpret_cast<float4*>(lds);  // [wave][rs][tt][lane]
+    // partial tiles into this wave's own region (its weight reads are done)
+    float4* red = reinterpret_cast<float4*>(region);
 #pragma unroll
     for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt)
         if (tt < ntiles)
-          red[((wave * RS + rs) * NT + tt) * 64 + lane] =
+          red[(rs * NT + tt) * 64 + u.lane] =
               float4{tot[rs][tt][0], tot[rs][tt][1], tot[rs][tt][2], tot[rs][tt][3]};
     __syncthreads();
-
-    // 5. epilogue: lane (r16, kq) of tile tt holds rows tt*16 + 4*kq + i, column r16
-    bool stored = false;
-    if constexpr (PH == 0) {
-      const int tt = wave;
-      if (tt < ntiles) {
-        float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int w = 0; w < DW; ++w) {
-          const float4 pg = red[((w * RS + 0) * NT + tt) * 64 + lane];
-          const float4 pu = red[((w * RS + 1) * NT + tt) * 64 + lane];
-          g[0] += pg.x; g[1] += pg.y; g[2] += pg.z; g[3] += pg.w;
-          u[0] += pu.x; u[1] += pu.y; u[2] += pu.z; u[3] += pu.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int q = tt * 16 + kq * 4 + i;
-          if (q < cc) {
-            const float v = silu_f32(g[i] * rowscale[0]) * (u[i] * rowscale[1]);
-            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)to_act_bits<BF>(v), mid_r,
-                                                  (rsl[q] * a.I + blk * 16 + r16) * 2, 0, CPOL_SC1);
-          }
-        }
-        stored = true;
-      }
-    } else {
-      for (int it = threadIdx.x; it < RS * ntiles * 64; it += DNT) {
-        const int rt = it >> 6;
-        const int rs = rt / ntiles, tt = rt - rs * ntiles;
-        float s[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int w = 0; w < DW; ++w) {
-          const float4 pv = red[((w * RS + rs) * NT + tt) * 64 + lane];
-          s[0] += pv.x; s[1] += pv.y; s[2] += pv.z; s[3] += pv.w;
-        }
-        float rsc = 1.f;
-#pragma unroll
-        for (int j = 0; j < RS; ++j)
-          if (j == rs) rsc = rowscale[j];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int q = tt * 16 + kq * 4 + i;
-          if (q < cc)
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s[i] * rsc), part_r,
-                                                  (rsl[q] * a.H + blk * ROWS_B + rs * 16 + r16) * 4,
-                                                  0, CPOL_SC1);
-        }
-        stored = true;
-      }
-    }
-    if (stored) wait_vm_all();  // this wave's shared stores have completed
-    __syncthreads();  // red / staging area and row_slot free again
-  }
-
-  // 6. publish
-  if constexpr (PH == 0) {
-    if (threadIdx.x == 0)
-      __hip_atomic_fetch_add(sync_a(a, e), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    if (threadIdx.x == 0) {
-      const int old =
-          __hip_atomic_fetch_add(sync_c(a, blk), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *s_flag = old == n_active - 1;
-    }
-    __syncthreads();
-    if (*s_flag) {
-      // Last down unit of this column block: combine it.
-      const int h0 = blk * ROWS_B;
-      for (int idx = threadIdx.x; idx < a.T * (ROWS_B / 4); idx += DNT) {
-        const int t = idx / (ROWS_B / 4);
-        const int h = h0 + (idx - t * (ROWS_B / 4)) * 4;
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < a.kp; ++j) {
-          float wgt = 1.f;
-          if (j < a.k) {
-            const int64_t id = load_index(a.ids, a.ids_dtype, (int64_t)t * a.k + j);
-            if (id < 0 || id >= a.E) continue;
-            wgt = load_as_f32(a.topk_w, a.w_dtype, (int64_t)t * a.k + j);
-          }
-          const float4 pv = __builtin_bit_cast(
-              float4, __builtin_amdgcn_raw_buffer_load_b128(
-                          part_r, ((t * a.kp + j) * a.H + h) * 4, 0, CPOL_SC1));
-          acc[0] += wgt * pv.x;
-          acc[1] += wgt * pv.y;
-          acc[2] += wgt * pv.z;
-          acc[3] += wgt * pv.w;
-        }
-        uint2 o;
-        o.x = to_act_bits<BF>(acc[0]) | (to_act_bits<BF>(acc[1]) << 16);
-        o.y = to_act_bits<BF>(acc[2]) | (to_act_bits<BF>(acc[3]) << 16);
-        *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.H + h) = o;
-      }
-      __syncthreads();
-      if (threadIdx.x == 0) {
-        __hip_atomic_store(sync_c(a, blk), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int d =
-            __hip_atomic_fetch_add(sync_done(a), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *s_flag = d == a.nbB - 1;
-      }
-      __syncthreads();
-      if (*s_flag) {  // every block is combined: no wait is pending, reset the counters
-        for (int i = threadIdx.x; i < a.Ep; i += DNT)
-          __hip_atomic_store(sync_a(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (threadIdx.x == 0)
-          __hip_atomic_store(sync_done(a), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    finish_pass<2, BF, PH, NT>(a, u, lds, sl, cc, ntiles, blk);
+    __syncthreads();  // LDS regions free again
   }
 }
 
-template <bool BF, int NT, bool MIXED>
-__global__ void __launch_bounds__(DNT, 2) moe_layer_kernel(LayerArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
-  __shared__ uint32_t bitmap[MAX_BM_WORDS];
-  __shared__ int s_ids[64 * MAX_ID_REGS];
-  __shared__ int row_slot[64 * MAX_ID_REGS];
-  __shared__ int s_flag;
-  const int lane = threadIdx.x & 63;
-  const int n = a.T * a.k;
-  const int nw = (a.Ep + 31) >> 5;
-
-  // 1. the routed ids into LDS (ids outside [0, E) become -1) and the
-  //    active-expert bitmap (shared experts are always active)
-  if (threadIdx.x < MAX_BM_WORDS) bitmap[threadIdx.x] = 0u;
-  __syncthreads();
-  for (int s = threadIdx.x; s < n; s += DNT) {
-    const int64_t id = load_index(a.ids, a.ids_dtype, s);
-    const int v = (id >= 0 && id < a.E) ? (int)id : -1;
-    s_ids[s] = v;
-    if (v >= 0) atomicOr(&bitmap[v >> 5], 1u << (v & 31));
-  }
-  if (threadIdx.x < a.Ep - a.E && a.T > 0)
-    atomicOr(&bitmap[(a.E + threadIdx.x) >> 5], 1u << ((a.E + threadIdx.x) & 31));
-  __syncthreads();
-  const uint32_t word = lane < nw ? bitmap[lane] : 0u;
-  const int c = __popc(word);
-  int incl = c;
+// General unit (any tier, any K): each wave streams k-blocks lo .. lo+nmy-1
+// through a register ring of P k-blocks.  Every ring slot is refilled
+// unconditionally: a k-block beyond the wave's range is read through a
+// zero-length buffer resource, which returns zeros without a memory access
+// (and contributes exactly zero), so the number of loads in flight is the
+// same on every path and each slot waits only for its own loads.  The first
+// ring fill of weights is issued before the expert's rows are gathered.
+template <int TIER, bool BF, int PH, int NT>
+__device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& rt, int e, int blk,
+                                              unsigned char* lds) {
+  using G = Geo<TIER, PH, NT>;
+  constexpr int RS = G::RS, QPK = G::QPK, P = G::P, WSLOT = G::WSLOT;
+  const UnitCtx<TIER, PH, NT> u(a, e, blk);
+  int voff[RS], soff[RS];
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(incl, d, 64);
-    if (lane >= d) incl += y;
+  for (int rs = 0; rs < RS; ++rs) {
+    const int row = u.row(a, blk, rs * 16 + u.r16);
+    voff[rs] = row * u.rowbytes + u.kq * 16 * QPK;
+    soff[rs] = row * u.ng * 2;
   }
-  const int n_active = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));
+  const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(dq_magic));
 
+  uint4 wreg[P][WSLOT];
+  uint32_t sreg[P][RS];
+  uint4 areg[P][4 * NT];
+  int xo[NT];
+  auto load_w = [&](int p, int kbl) {
+    const bool ok = kbl < u.nmy;
+    const __amdgpu_buffer_rsrc_t r = ok ? u.wr : u.wnull;
+    const int kb = ok ? u.lo + kbl : u.lo;
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+#pragma unroll
+      for (int h = 0; h < QPK; ++h)
+        wreg[p][rs * QPK + h] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff[rs] + h * 16, kb * G::KBSTRIDE, 0));
+      if constexpr (TIER == 2)
+        sreg[p][rs] = __builtin_amdgcn_raw_buffer_load_b16(ok ? u.sr : u.snull, soff[rs],
+                                                           (kb >> a.gshift) * 2, 0);
+    }
+  };
+  auto load_a = [&](int p, int kbl) {
+    const bool ok = kbl < u.nmy;
+    const int kb = ok ? u.lo + kbl : u.lo;
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        areg[p][tt * 4 + d] = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(ok ? u.xr : u.xnull, xo[tt] + d * 16,
+                                                         kb * 256, 0));
+  };
+
+#pragma unroll
+  for (int p = 0; p < P; ++p) load_w(p, p);
+  int sl[NT];
+  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, 0, sl));
+
+  for (int r0 = 0; r0 < cnt; r0 += NT * 16) {
+    const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
+    const int ntiles = (cc + 15) >> 4;
+    if (r0 > 0) {  // a further pass streams the weights again
+#pragma unroll
+      for (int p = 0; p < P; ++p) load_w(p, p);
+      lane_slots<NT>(a, rt, e, r0, sl);
+    }
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) xo[tt] = u.xoff(a, sl[tt]);
+#pragma unroll
+    for (int p = 0; p < P; ++p) load_a(p, p);
+
+    f32x4_t tot[RS][NT];
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) tot[rs][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb0 = 0; kb0 < u.nmy; kb0 += P) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        // One row set's weights as MFMA B operands (exact base + q values).
+        auto dequant = [&](int rs, uint4 (&bfr)[4], float& sc) {
+          sc = 1.f;
+          if constexpr (TIER == 2) {
+            const uint4 w = wreg[p][rs];
+            bfr[0] = ddeq4(w.x, dq_mask, dq_magic);
+            bfr[1] = ddeq4(w.y, dq_mask, dq_magic);
+            bfr[2] = ddeq4(w.z, dq_mask, dq_magic);
+            bfr[3] = ddeq4(w.w, dq_mask, dq_magic);
+            sc = f16_bits_to_f32(sreg[p][rs]);
+          } else if constexpr (TIER == 1) {
+            const uint4 w0 = wreg[p][rs * QPK + 0], w1 = wreg[p][rs * QPK + 1];
+            const uint2 d0 = ddeq8<BF>(w0.x), d1 = ddeq8<BF>(w0.y);
+            const uint2 d2 = ddeq8<BF>(w0.z), d3 = ddeq8<BF>(w0.w);
+            const uint2 d4 = ddeq8<BF>(w1.x), d5 = ddeq8<BF>(w1.y);
+            const uint2 d6 = ddeq8<BF>(w1.z), d7 = ddeq8<BF>(w1.w);
+            bfr[0] = uint4{d0.x, d0.y, d1.x, d1.y};
+            bfr[1] = uint4{d2.x, d2.y, d3.x, d3.y};
+            bfr[2] = uint4{d4.x, d4.y, d5.x, d5.y};
+            bfr[3] = uint4{d6.x, d6.y, d7.x, d7.y};
+          } else {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) bfr[h] = wreg[p][rs * QPK + h];
+          }
+        };
+        if constexpr (NT == 1) {
+          // A operand first, then one row set at a time
+          uint4 xa[4];
+          f32x4_t init;
+          make_a<TIER, BF, PH>(&areg[p][0], xa, init);
+#pragma unroll
+          for (int rs = 0; rs < RS; ++rs) {
+            uint4 bfr[4];
+            float sc;
+            dequant(rs, bfr, sc);
+            f32x4_t acc = init;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) acc = dmfma<BF>(xa[d], bfr[d], acc);
+            tot[rs][0] += sc * acc;
+          }
+        } else {
+          // several tiles: one tile's A operand at a time (fewer live registers)
+#pragma unroll
+          for (int tt = 0; tt < NT; ++tt) {
+            if (tt < ntiles) {
+              uint4 xa[4];
+              f32x4_t init;
+              make_a<TIER, BF, PH>(&areg[p][tt * 4], xa, init);
+#pragma unroll
+              for (int rs = 0; rs < RS; ++rs) {
+                uint4 bfr[4];
+                float sc;
+                dequant(rs, bfr, sc);
+                f32x4_t acc = init;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) acc = dmfma<BF>(xa[d], bfr[d], acc);
+                tot[rs][tt] += sc * acc;
+              }
+            }
+          }
+        }
+        load_w(p, kb0 + p + P);  // refill this ring slot (zeros past the range)
+        load_a(p, kb0 + p + P);
+        // keep the ring order: slot p's refill is issued before slot p+1 is consumed
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    float4* red = reinterpret_cast<float4*>(lds + u.wave * WAVE_LDS);
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+        if (tt < ntiles)
+          red[(rs * NT + tt) * 64 + u.lane] =
+              float4{tot[rs][tt][0], tot[rs][tt][1], tot[rs][tt][2], tot[rs][tt][3]};
+    __syncthreads();
+    finish_pass<TIER, BF, PH, NT>(a, u, lds, sl, cc, ntiles, blk);
+    __syncthreads();  // LDS regions free again
+  }
+}
+
+// A grid of at most one resident round of work-groups; each routes once and
+// then takes units blockIdx.x, blockIdx.x + gridDim.x, ... (expert-major:
+// unit u is row block u % nb of the (u / nb)-th active expert).
+template <bool BF, int PH, int NT, bool MIXED, bool DMA>
+__global__ void __launch_bounds__(DNT, 2) moe_decode_kernel(LayerArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
+  __shared__ Route rt;
+  __shared__ int s_flag;
+  uint32_t word;
+  int incl, c;
+  const int n_active = route(a, rt, word, incl, c);
   if (n_active == 0) {  // nothing routed: the output is zero
-    uint4* o = reinterpret_cast<uint4*>(a.out);
-    const int64_t n16 = (int64_t)a.T * a.H / 8;
-    for (int64_t i = (int64_t)blockIdx.x * DNT + threadIdx.x; i < n16; i += (int64_t)gridDim.x * DNT)
-      o[i] = uint4{0u, 0u, 0u, 0u};
+    if (PH == 1) {
+      uint4* o = reinterpret_cast<uint4*>(a.out);
+      const int64_t n16 = (int64_t)a.T * a.H / 8;
+      for (int64_t i = (int64_t)blockIdx.x * DNT + threadIdx.x; i < n16;
+           i += (int64_t)gridDim.x * DNT)
+        o[i] = uint4{0u, 0u, 0u, 0u};
+    }
     return;
   }
-
-  const int NA = n_active * a.nbA, NB = n_active * a.nbB;
-  for (int u = blockIdx.x; u < NA + NB; u += gridDim.x) {
-    const int ph = u >= NA;
-    const int uu = ph ? u - NA : u;
-    const int nb = ph ? a.nbB : a.nbA;
-    const int ai = uu / nb;
-    const int blk = uu - ai * nb;
-
-    // 3. the ai-th active expert
-    const uint64_t hit = __ballot(incl - c <= ai && ai < incl);
-    const int wl = __ffsll((unsigned long long)hit) - 1;
-    uint32_t wbits = __shfl(word, wl, 64);
-    const int q0 = ai - (__shfl(incl, wl, 64) - __shfl(c, wl, 64));
-    for (int t = 0; t < q0; ++t) wbits &= wbits - 1u;
-    const int e = __builtin_amdgcn_readfirstlane(wl * 32 + (__ffs(wbits) - 1));
-
-    // 4. the expert's slots in ascending order (extended slot t*kp + j), as a
-    //    table in LDS.  A token routed twice to one expert (repeated ids) adds
-    //    rows; cnt <= T*k <= 1024.
-    __syncthreads();  // the previous unit is done with row_slot
-    int cnt;
-    if (e < a.E) {
-      uint64_t m[MAX_ID_REGS];
-      int pre[MAX_ID_REGS + 1];
-      pre[0] = 0;
-#pragma unroll
-      for (int i = 0; i < MAX_ID_REGS; ++i) {
-        m[i] = 64 * i < n ? __ballot(lane + 64 * i < n && s_ids[lane + 64 * i] == e) : 0ull;
-        pre[i + 1] = pre[i] + __popcll(m[i]);
-      }
-      cnt = pre[MAX_ID_REGS];
-      for (int r = threadIdx.x; r < cnt; r += DNT) {
-        int i = 0;
-#pragma unroll
-        for (int j = 1; j < MAX_ID_REGS; ++j) i = (r >= pre[j]) ? j : i;
-        uint64_t mi = m[0];
-        int pi = 0;
-#pragma unroll
-        for (int j = 1; j < MAX_ID_REGS; ++j) {
-          if (j == i) {
-            mi = m[j];
-            pi = pre[j];
-          }
-        }
-        const int s = 64 * i + nth_set_bit(mi, r - pi);
-        const int t = s / a.k;
-        row_slot[r] = t * a.kp + (s - t * a.k);
-      }
-    } else {
-      cnt = a.T;
-      for (int r = threadIdx.x; r < cnt; r += DNT) row_slot[r] = r * a.kp + a.k + (e - a.E);
-    }
-    __syncthreads();
-
-    const int tier = MIXED ? (int)a.tier[e] : 2;
+  const int nb = PH == 0 ? a.nbA : a.nbB;
+  const int n_units = n_active * nb;
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {  // uniform across the work-group
+    const int ai = u / nb;
+    const int blk = u - ai * nb;
+    const int e = select_expert(ai, word, incl, c);
+    const int tier = MIXED ? __builtin_amdgcn_readfirstlane((int)a.tier[e]) : 2;
     if (!MIXED || tier == 2) {
-      if (ph == 0)
-        unit_body<2, BF, 0, NT>(a, e, blk, cnt, row_slot, dyn_lds, &s_flag, n_active);
+      if constexpr (DMA)
+        run_unit_dma<BF, PH, NT>(a, rt, e, blk, dyn_lds);
       else
-        unit_body<2, BF, 1, NT>(a, e, blk, cnt, row_slot, dyn_lds, &s_flag, n_active);
-    } else if (tier == 1) {
-      if (ph == 0)
-        unit_body<1, BF, 0, NT>(a, e, blk, cnt, row_slot, dyn_lds, &s_flag, n_active);
+        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, dyn_lds);
+    } else if constexpr (MIXED) {
+      if (tier == 1)
+        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, dyn_lds);
       else
-        unit_body<1, BF, 1, NT>(a, e, blk, cnt, row_slot, dyn_lds, &s_flag, n_active);
-    } else {
-      if (ph == 0)
-        unit_body<0, BF, 0, NT>(a, e, blk, cnt, row_slot, dyn_lds, &s_flag, n_active);
-      else
-        unit_body<0, BF, 1, NT>(a, e, blk, cnt, row_slot, dyn_lds, &s_flag, n_active);
+        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, dyn_lds);
     }
+    if constexpr (PH == 1) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_active, &s_flag);
   }
 }
 
-typedef void (*layer_kernel_t)(LayerArgs);
+typedef void (*decode_kernel_t)(LayerArgs);
 
-template <bool BF, int NT>
-layer_kernel_t pick_nt(bool mixed) {
-  return mixed ? moe_layer_kernel<BF, NT, true> : moe_layer_kernel<BF, NT, false>;
+template <bool BF, int PH, bool MIXED, bool DMA>
+decode_kernel_t pick_nt(int nt) {
+  if (nt == 1) return moe_decode_kernel<BF, PH, 1, MIXED, DMA>;
+  if (nt == 2) return moe_decode_kernel<BF, PH, 2, MIXED, DMA>;
+  return moe_decode_kernel<BF, PH, 4, MIXED, DMA>;
 }
 
-layer_kernel_t pick_kernel(bool bf, int nt, bool mixed) {
-  if (bf) {
-    if (nt == 1) return pick_nt<true, 1>(mixed);
-    if (nt == 2) return pick_nt<true, 2>(mixed);
-    return pick_nt<true, 4>(mixed);
-  }
-  if (nt == 1) return pick_nt<false, 1>(mixed);
-  if (nt == 2) return pick_nt<false, 2>(mixed);
-  return pick_nt<false, 4>(mixed);
+template <bool BF, int PH>
+decode_kernel_t pick_ph(int nt, bool mixed, bool dma) {
+  if (mixed) return dma ? pick_nt<BF, PH, true, true>(nt) : pick_nt<BF, PH, true, false>(nt);
+  return dma ? pick_nt<BF, PH, false, true>(nt) : pick_nt<BF, PH, false, false>(nt);
 }
 
-// Co-resident work-groups per CU for (kernel, dynamic LDS), cached.
-struct OccEntry {
-  const void* fn;
-  size_t lds;
-  int dev;
-  int blocks;
-};
-std::mutex g_occ_mu;
-OccEntry g_occ[64];
-int g_occ_n = 0;
-
-int resident_blocks(layer_kernel_t fn, size_t lds, int* out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return set_error(EXQ_ERROR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
-  {
-    std::lock_guard<std::mutex> g(g_occ_mu);
-    for (int i = 0; i < g_occ_n; ++i)
-      if (g_occ[i].fn == (const void*)fn && g_occ[i].lds == lds && g_occ[i].dev == dev) {
-        *out = g_occ[i].blocks;
-        return EXQ_SUCCESS;
-      }
-  }
-  int per_cu = 0, n_cu = 0;
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(fn),
-                                                   DNT, lds);
-  if (e != hipSuccess)
-    return set_error(EXQ_ERROR_HIP, "occupancy query: %s", hipGetErrorString(e));
-  e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e != hipSuccess)
-    return set_error(EXQ_ERROR_HIP, "CU count query: %s", hipGetErrorString(e));
-  if (per_cu < 1 || n_cu < 1)
-    return set_error(EXQ_ERROR_UNSUPPORTED, "moe_layer_kernel cannot be resident (%d per CU)",
-                     per_cu);
-  *out = per_cu * n_cu;
-  std::lock_guard<std::mutex> g(g_occ_mu);
-  if (g_occ_n < 64) g_occ[g_occ_n++] = OccEntry{(const void*)fn, lds, dev, *out};
-  return EXQ_SUCCESS;
+decode_kernel_t pick_kernel(bool bf, int ph, int nt, bool mixed, bool dma) {
+  if (bf) return ph == 0 ? pick_ph<true, 0>(nt, mixed, dma) : pick_ph<true, 1>(nt, mixed, dma);
+  return ph == 0 ? pick_ph<false, 0>(nt, mixed, dma) : pick_ph<false, 1>(nt, mixed, dma);
 }
 
 }  // namespace
 
+// Work-groups of `kern` that fit on the device at once (CUs x per-CU
+// occupancy), cached per (device, kernel, LDS bytes).
+int resident_work_groups(const void* kern, int threads, size_t lds, int* out) {
+  static std::mutex mu;
+  static std::map<std::tuple<int, const void*, size_t>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(EXQ_ERROR_HIP, "decode: hipGetDevice failed");
+  const auto key = std::make_tuple(dev, kern, lds);
+  {
+    std::lock_guard<std::mutex> g(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) {
+      *out = it->second;
+      return EXQ_SUCCESS;
+    }
+  }
+  int cus = 0, per = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, threads, lds) != hipSuccess)
+    return set_error(EXQ_ERROR_HIP, "decode: occupancy query failed");
+  const int n = cus * per > 0 ? cus * per : 1;
+  std::lock_guard<std::mutex> g(mu);
+  cache[key] = n;
+  *out = n;
+  return EXQ_SUCCESS;
+}
+
 bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, int64_t H,
                            int64_t group_size) {
   const int64_t gkb = group_size / 128;  // k-blocks per scale group: a power of two
-  return T >= 1 && T <= 64 && T * k <= 64 * MAX_ID_REGS && Ep <= kDecodeMaxBuckets &&
+  return T >= 1 && T <= 64 && T * k <= MAX_SLOTS && Ep <= kDecodeMaxBuckets &&
          n_shared <= 64 && H / 32 <= kDecodeMaxHBlocks && H % 64 == 0 && gkb >= 1 &&
          (gkb & (gkb - 1)) == 0;
 }
@@ -787,27 +953,32 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   a.part = d.part;
   a.out = d.out;
   a.sync = d.sync;
-  // A pass holds NT*16 rows; each wave stages its k-range of those rows in
-  // an LDS region of xw 16-bit elements (at least one k-block of a full pass).
+  const bool mixed = d.tier != nullptr;
   const int nt = d.T <= 16 ? 1 : (d.T <= 32 ? 2 : 4);
   a.nbA = d.I / 16;
   a.nbB = d.H / rows_b(nt);
-  const int xw_min = nt * 16 * 128;
-  a.xw = xw_min > 4096 ? xw_min : 4096;
-  size_t lds = (size_t)DW * a.xw * 2;
-  const size_t red = (size_t)DW * (rows_b(nt) / 16) * nt * 64 * 16;
-  if (red > lds) lds = red;
-
-  layer_kernel_t fn = pick_kernel(d.bf, nt, d.tier != nullptr);
-  int resident = 0;
-  int st = resident_blocks(fn, lds, &resident);
-  if (st) return st;
   const int64_t max_active = (int64_t)(d.T * d.k < d.E ? d.T * d.k : d.E) + (d.Ep - d.E);
-  const int64_t units = max_active * (a.nbA + a.nbB);
-  int64_t grid = units < resident ? units : resident;
-  if (grid < 1) grid = 1;
-  hipLaunchKernelGGL(fn, dim3((unsigned)grid), dim3(DNT), lds, s, a);
-  return check_launch("moe_layer_kernel");
+  for (int ph = 0; ph < 2; ++ph) {
+    const size_t lds = (size_t)DW * WAVE_LDS;  // per-wave weight slices / partial tiles
+    // INT4 slices go through LDS when every wave's k-range fits its region
+    const int rs = ph == 0 ? 2 : rows_b(nt) / 16;
+    const int nkb = (ph == 0 ? d.H : d.I) / 128;
+    const bool dma = (nkb + 3) / 4 <= WAVE_LDS / (rs * 1024);
+    const decode_kernel_t kern = pick_kernel(d.bf, ph, nt, mixed, dma);
+    const int64_t units = max_active * (ph == 0 ? a.nbA : a.nbB);
+    int resident = 0;
+    const int st0 = resident_work_groups(reinterpret_cast<const void*>(kern), DNT, lds, &resident);
+    if (st0) return st0;
+    const int64_t grid = units < resident ? units : resident;
+    const dim3 g((unsigned)(grid > 0 ? grid : 1));
+    if (const hipEvent_t* ev = stage_events())  // start / stop of exactly this kernel
+      hipExtLaunchKernelGGL(kern, g, dim3(DNT), lds, s, ev[2 * ph], ev[2 * ph + 1], 0, a);
+    else
+      hipLaunchKernelGGL(kern, g, dim3(DNT), lds, s, a);
+    const int st = check_launch(ph == 0 ? "moe_decode_kernel<gate/up>" : "moe_decode_kernel<down>");
+    if (st) return st;
+  }
+  return EXQ_SUCCESS;
 }
 
 }  // namespace exq

@@ -90,4 +90,8 @@ bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, i
                            int64_t group_size);
 int launch_decode_layer(const DecodeLaunch& d, hipStream_t s);
 
+// The four stage events installed with exq_set_stage_events for the current
+// call on this thread, or nullptr.
+const hipEvent_t* stage_events();
+
 }  // namespace exq

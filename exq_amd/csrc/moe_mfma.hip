@@ -472,6 +472,12 @@ int record_stage(int i, hipStream_t s) {
   return EXQ_SUCCESS;
 }
 
+}  // namespace
+
+const hipEvent_t* stage_events() { return g_stage_events_set ? g_stage_events : nullptr; }
+
+namespace {
+
 // ---- workspace layout of the fused forward --------------------------------------
 struct FusedLayout {
   size_t sync, hdr, ends, sorted, tg, mid, partial, total;
@@ -570,16 +576,21 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   } hook_reset;
   const bool decode =
       decode_path_supported(T, k, Ep, p->n_shared, p->hidden_size, p->group_size);
-  int st = record_stage(0, s);
-  if (st) return st;
-  // The decode path routes inside its persistent kernel; the routing plan
-  // runs only when the caller asked for the routing arrays.
+  int st = EXQ_SUCCESS;
+  if (!decode) {
+    st = record_stage(0, s);
+    if (st) return st;
+  }
+  // The decode kernels route for themselves; the routing plan runs only when
+  // the caller asked for the routing arrays.
   if (!decode || sort_order_out || expert_ends_out) {
     st = launch_route_plan(rp, s);
     if (st) return st;
   }
-  st = record_stage(1, s);
-  if (st) return st;
+  if (!decode) {
+    st = record_stage(1, s);
+    if (st) return st;
+  }
 
   if (decode) {
     DecodeLaunch d{};
@@ -601,11 +612,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     d.out = reinterpret_cast<uint16_t*>(out);
     d.sync = reinterpret_cast<int*>(ws + L.sync);
     d.bf = bf;
-    st = launch_decode_layer(d, s);
-    if (st) return st;
-    st = record_stage(2, s);
-    if (st) return st;
-    return record_stage(3, s);
+    return launch_decode_layer(d, s);  // times its two kernels with the stage events
   } else {
     GemmArgs g{};
     g.hdr = rp.hdr;

@@ -226,8 +226,8 @@ typedef struct exq_expert_bank {
 
 /*
  * Workspace bytes needed by the fused entry points for this problem.  The
- * first bytes of a fused-layer workspace hold synchronisation counters of the
- * one-launch decode kernel (T <= 64): the workspace must be zero-filled
+ * first bytes of a fused-layer workspace hold the combine counters of the
+ * decode kernels (T <= 64): the workspace must be zero-filled
  * before its first use, every call leaves those counters zero again, and a
  * workspace must not be shared by calls that may run concurrently or with
  * other entry points.
@@ -237,8 +237,9 @@ size_t exq_moe_workspace_size(const exq_moe_problem* problem);
 /*
  * The whole INT4 MoE layer: routing preparation, gate/up INT4 GEMM fused with
  * SiLU-and-mul, down INT4 GEMM, top-k weighted combine.  Decode batches
- * (T <= 64) run as one persistent kernel; larger batches as routing plan +
- * two grouped MFMA GEMMs + combine.  Replaces the
+ * (T <= 64) run as two kernels (gate/up + SiLU, down + combine) that route
+ * for themselves; larger batches as routing plan + two grouped MFMA GEMMs +
+ * combine.  Replaces the
  * pipeline of _exq_forward_cuda (exq/runtime/sglang_backend.py:65-158:
  * moe_align_block_size -> build_ends_from_slots -> gather_hidden -> GEMM1 ->
  * silu_and_mul -> GEMM2 -> combine) and moe_int4_full_forward
@@ -269,11 +270,14 @@ int exq_moe_mixed_forward(const exq_moe_problem* problem, const void* hidden,
 /*
  * Measurement hook (no counterpart in the reference, whose harness times whole
  * calls with perf_counter, exq/eval/bench.py:15-46).  When set on the calling
- * thread, the next fused / mixed forward records events[0] before the routing
- * kernel, events[1] before the gate/up kernel, events[2] before the down
- * kernel and events[3] after the combine kernel that follows it, on the
- * call's stream.  events are hipEvent_t
- * handles; pass (NULL, 0) to disable.  The hook is consumed by one call.
+ * thread, the next fused / mixed forward records hipEvent_t events on the
+ * call's stream.  Decode batches (two kernels): events[0] / events[1] are the
+ * start / stop of the gate/up kernel and events[2] / events[3] those of the
+ * down kernel, recorded by the launches themselves (hipExtLaunchKernelGGL),
+ * so each pair times exactly one kernel.  Larger batches: events[0] before the
+ * routing kernel, events[1] before the gate/up kernel, events[2] before the
+ * down kernel and events[3] after the combine kernel.  Pass (NULL, 0) to
+ * disable.  The hook is consumed by one call.
  */
 int exq_set_stage_events(void* const* events, int n_events);
 
