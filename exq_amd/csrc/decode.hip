@@ -878,22 +878,19 @@ __global__ void __launch_bounds__(DNT, 2) moe_decode_kernel(LayerArgs a) {
 
 typedef void (*decode_kernel_t)(LayerArgs);
 
-template <bool BF, int PH, bool MIXED, bool DMA>
-decode_kernel_t pick_nt(int nt) {
-  if (nt == 1) return moe_decode_kernel<BF, PH, 1, MIXED, DMA>;
-  if (nt == 2) return moe_decode_kernel<BF, PH, 2, MIXED, DMA>;
-  return moe_decode_kernel<BF, PH, 4, MIXED, DMA>;
-}
-
 template <bool BF, int PH>
-decode_kernel_t pick_ph(int nt, bool mixed, bool dma) {
-  if (mixed) return dma ? pick_nt<BF, PH, true, true>(nt) : pick_nt<BF, PH, true, false>(nt);
-  return dma ? pick_nt<BF, PH, false, true>(nt) : pick_nt<BF, PH, false, false>(nt);
+decode_kernel_t pick_ph(bool mixed, bool dma) {
+  if (mixed) return dma ? moe_decode_kernel<BF, PH, 1, true, true> : moe_decode_kernel<BF, PH, 1, true, false>;
+  return dma ? moe_decode_kernel<BF, PH, 1, false, true> : moe_decode_kernel<BF, PH, 1, false, false>;
 }
 
-decode_kernel_t pick_kernel(bool bf, int ph, int nt, bool mixed, bool dma) {
-  if (bf) return ph == 0 ? pick_ph<true, 0>(nt, mixed, dma) : pick_ph<true, 1>(nt, mixed, dma);
-  return ph == 0 ? pick_ph<false, 0>(nt, mixed, dma) : pick_ph<false, 1>(nt, mixed, dma);
+// One 16-row tile per pass: units with more rows take further passes (each
+// re-reads its weight slice, from L2), which measured faster at T = 32 and 64
+// than kernels holding two or four tiles per pass (higher register use, lower
+// occupancy).
+decode_kernel_t pick_kernel(bool bf, int ph, bool mixed, bool dma) {
+  if (bf) return ph == 0 ? pick_ph<true, 0>(mixed, dma) : pick_ph<true, 1>(mixed, dma);
+  return ph == 0 ? pick_ph<false, 0>(mixed, dma) : pick_ph<false, 1>(mixed, dma);
 }
 
 }  // namespace
@@ -954,7 +951,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   a.out = d.out;
   a.sync = d.sync;
   const bool mixed = d.tier != nullptr;
-  const int nt = d.T <= 16 ? 1 : (d.T <= 32 ? 2 : 4);
+  const int nt = 1;
   a.nbA = d.I / 16;
   a.nbB = d.H / rows_b(nt);
   const int64_t max_active = (int64_t)(d.T * d.k < d.E ? d.T * d.k : d.E) + (d.Ep - d.E);
@@ -964,7 +961,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     const int rs = ph == 0 ? 2 : rows_b(nt) / 16;
     const int nkb = (ph == 0 ? d.H : d.I) / 128;
     const bool dma = (nkb + 3) / 4 <= WAVE_LDS / (rs * 1024);
-    const decode_kernel_t kern = pick_kernel(d.bf, ph, nt, mixed, dma);
+    const decode_kernel_t kern = pick_kernel(d.bf, ph, mixed, dma);
     const int64_t units = max_active * (ph == 0 ? a.nbA : a.nbB);
     int resident = 0;
     const int st0 = resident_work_groups(reinterpret_cast<const void*>(kern), DNT, lds, &resident);
