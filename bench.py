@@ -54,6 +54,8 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--cpu-reps", type=int, default=10)
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other BASELINE.json configurations")
     ap.add_argument("--pmc-run", action="store_true",
                     help="calibration copy + one eager pass, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summary", type=str, default="",
@@ -212,6 +214,183 @@ def stage_times(stack, b, reps=3):
     return {"gateup_us": mean(gateup), "down_us": mean(down), "layer_us": mean(layer)}
 
 
+MFMA_PEAK_BF16_TFLOPS = 2500.0
+
+
+def _graph_time(fn, reps, warmup=3):
+    """Mean ms per call of `fn` replayed from a HIP graph."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def measure_configs(dev, reps):
+    """The other BASELINE.json configurations: decode µs/layer and achieved GB/s
+    on activated-expert bytes (weights + scales; shared experts included) over
+    distinct seeded layers replayed from a HIP graph, and prefill TFLOP/s."""
+    import numpy as np
+    import torch
+    from exq_amd import synth
+    from exq_amd.kernels import (MixedExpertBank, fused_experts, fused_experts_mixed,
+                                 pack_experts_int4)
+    from exq_amd.kernels.fused_moe import moe_workspace_bytes
+    rows = []
+
+    def ws_for(cfg, T):  # explicit workspace: nothing allocates inside graph capture
+        return torch.zeros(moe_workspace_bytes(T, cfg.hidden, cfg.inter, cfg.n_experts,
+                                               cfg.top_k, cfg.n_shared), dtype=torch.uint8,
+                           device=dev)
+
+    def decode_row(name, cfg, T, calls, bytes_per_call, n_layers):
+        ms = _graph_time(lambda: [c() for c in calls], reps)
+        us = ms * 1e3 / len(calls)
+        gbps = bytes_per_call / (us * 1e-6) / 1e9
+        rows.append({"config": name, "batch": T, "layers_rotated": n_layers,
+                     "us_per_layer": round(us, 2), "tokens_per_s": round(T / (us * 1e-6)),
+                     "achieved_GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)})
+        log(f"config {name} T={T}: {us:.2f} us/layer, {gbps:.0f} GB/s")
+
+    def prefill_row(name, T, fn, flops):
+        ms = _graph_time(fn, max(3, reps // 10))
+        tf = flops / (ms * 1e-3) / 1e12
+        rows.append({"config": name, "batch": T, "us_per_layer": round(ms * 1e3, 1),
+                     "tokens_per_s": round(T / (ms * 1e-3)), "TFLOPs": round(tf, 1),
+                     "frac_of_mfma_peak": round(tf / MFMA_PEAK_BF16_TFLOPS, 4)})
+        log(f"config {name} prefill T={T}: {ms * 1e3:.1f} us/layer, {tf:.1f} TFLOP/s")
+
+    def routing_for(cfg, T, layer):
+        ids, w = synth.routing(cfg, T, layer)
+        return (torch.from_numpy(ids.astype(np.int32)).to(dev), torch.from_numpy(w).to(dev),
+                ids)
+
+    def int4_layers(cfg, n_layers):
+        out = []
+        for l in range(n_layers):
+            w13, w2 = synth.expert_weights_gpu(cfg.n_experts, cfg.inter, cfg.hidden,
+                                               synth.seed_for(cfg, l), dev)
+            out.append(pack_experts_int4(w13) + pack_experts_int4(w2))
+            del w13, w2
+        return out
+
+    # OLMoE single INT4 layer (configs[0]); 3 distinct layers so the 198 MiB
+    # bank does not sit in the 256 MB Infinity Cache between calls
+    cfg = synth.CONFIGS["olmoe"]
+    layers = int4_layers(cfg, 3)
+    eb = synth.int4_expert_bytes(cfg.hidden, cfg.inter, cfg.group_size)
+    for T in (1, 16, 64):
+        x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 77 + T)).to(torch.bfloat16).to(dev)
+        ws = ws_for(cfg, T)
+        calls, nbytes = [], 0
+        for l, (p13, s13, p2, s2) in enumerate(layers):
+            tid, tw, ids = routing_for(cfg, T, l)
+            nbytes += np.unique(ids).size * eb
+            calls.append(lambda p13=p13, s13=s13, p2=p2, s2=s2, tw=tw, tid=tid, x=x, ws=ws:
+                         fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws))
+        decode_row("olmoe", cfg, T, calls, nbytes / len(layers), len(layers))
+    del layers
+    torch.cuda.empty_cache()
+
+    # Mixed-precision OLMoE stack (configs[2]): 16 layers, BF16/INT8/INT4 per layer
+    cfg = synth.CONFIGS["mixed_olmoe"]
+    banks = []
+    for l in range(cfg.n_layers):
+        w13, w2 = synth.expert_weights_gpu(cfg.n_experts, cfg.inter, cfg.hidden,
+                                           synth.seed_for(cfg, l), dev)
+        banks.append(MixedExpertBank.from_weights(w13, w2,
+                                                  synth.mixed_tiers(cfg.n_experts,
+                                                                    synth.seed_for(cfg, l))))
+        del w13, w2
+    T = 32
+    x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 99)).to(torch.bfloat16).to(dev)
+    ws = ws_for(cfg, T)
+    calls, nbytes = [], 0
+    for l, bank in enumerate(banks):
+        tid, tw, ids = routing_for(cfg, T, l)
+        nbytes += sum(bank.stored_bytes(int(e)) for e in np.unique(ids))
+        calls.append(lambda bank=bank, tw=tw, tid=tid: fused_experts_mixed(x, bank, tw, tid,
+                                                                         workspace=ws))
+    decode_row("mixed_olmoe", cfg, T, calls, nbytes / len(banks), len(banks))
+    del banks
+    torch.cuda.empty_cache()
+
+    # DeepSeek-V2-Lite: 64 INT4 routed experts + 2 BF16 shared (configs[3])
+    cfg = synth.CONFIGS["deepseek_v2_lite"]
+    banks = []
+    for l in range(3):
+        w13, w2 = synth.expert_weights_gpu(cfg.n_experts, cfg.inter, cfg.hidden,
+                                           synth.seed_for(cfg, l), dev)
+        s13, s2 = synth.expert_weights_gpu(cfg.n_shared, cfg.inter, cfg.hidden,
+                                           synth.seed_for(cfg, l) + 500, dev)
+        banks.append(MixedExpertBank.from_weights(w13, w2, [2] * cfg.n_experts, shared_w13=s13,
+                                                  shared_w2=s2, shared_tier=0))
+        del w13, w2, s13, s2
+    shared_bytes = cfg.n_shared * synth.bf16_expert_bytes(cfg.hidden, cfg.inter)
+    eb = synth.int4_expert_bytes(cfg.hidden, cfg.inter, cfg.group_size)
+    for T in (1, 16, 64):
+        x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 55 + T)).to(torch.bfloat16).to(dev)
+        ws = ws_for(cfg, T)
+        calls, nbytes = [], 0
+        for l, bank in enumerate(banks):
+            tid, tw, ids = routing_for(cfg, T, l)
+            nbytes += np.unique(ids).size * eb + shared_bytes
+            calls.append(lambda bank=bank, tw=tw, tid=tid, x=x, ws=ws:
+                         fused_experts_mixed(x, bank, tw, tid, workspace=ws))
+        decode_row("deepseek_v2_lite", cfg, T, calls, nbytes / len(banks), len(banks))
+    T = 2048
+    x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 3)).to(torch.bfloat16).to(dev)
+    tid, tw, _ = routing_for(cfg, T, 0)
+    ws = ws_for(cfg, T)
+    flops = 2.0 * T * (cfg.top_k + cfg.n_shared) * 3 * cfg.hidden * cfg.inter
+    prefill_row("deepseek_v2_lite", T,
+                lambda: fused_experts_mixed(x, banks[0], tw, tid, workspace=ws), flops)
+    del banks
+    torch.cuda.empty_cache()
+
+    # Mixtral-8x7B: 8 huge INT4 experts, top-2 (configs[4]); 2 layers (1.45 GB)
+    cfg = synth.CONFIGS["mixtral"]
+    layers = int4_layers(cfg, 2)
+    eb = synth.int4_expert_bytes(cfg.hidden, cfg.inter, cfg.group_size)
+    for T in (1, 16, 64):
+        x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 11 + T)).to(torch.bfloat16).to(dev)
+        ws = ws_for(cfg, T)
+        calls, nbytes = [], 0
+        for l, (p13, s13, p2, s2) in enumerate(layers):
+            tid, tw, ids = routing_for(cfg, T, l)
+            nbytes += np.unique(ids).size * eb
+            calls.append(lambda p13=p13, s13=s13, p2=p2, s2=s2, tw=tw, tid=tid, x=x, ws=ws:
+                         fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws))
+        decode_row("mixtral", cfg, T, calls, nbytes / len(layers), len(layers))
+    T = 4096
+    x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 4)).to(torch.bfloat16).to(dev)
+    tid, tw, _ = routing_for(cfg, T, 0)
+    p13, s13, p2, s2 = layers[0]
+    ws = ws_for(cfg, T)
+    flops = 2.0 * T * cfg.top_k * 3 * cfg.hidden * cfg.inter
+    prefill_row("mixtral", T, lambda: fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws),
+                flops)
+    del layers
+    torch.cuda.empty_cache()
+    return rows
+
+
 def cpu_baseline(stack, b, reps):
     """The reference's PyTorch CPU path (oracle/cpu_baseline.py) on this host."""
     import torch
@@ -306,6 +485,11 @@ def main():
         log(f"sweep T={T}: {ul:.2f} us/layer, {g:.0f} GB/s")
         if bb is not b:
             del bb
+    configs = None
+    if not args.no_configs:
+        t1 = time.time()
+        configs = measure_configs(dev, max(20, args.steps))
+        log(f"configs measured in {time.time() - t1:.1f}s")
     cpu = None
     if not args.no_cpu:
         t1 = time.time()
@@ -342,6 +526,7 @@ def main():
                      "bytes_per_launch": round(kern_bytes), "launch_us": round(kern_us, 3)},
         "stages_us": {k: round(v, 3) for k, v in st.items()},
         "sweep": sweep,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
