@@ -58,7 +58,7 @@ _SIGNATURES = {
     "exq_combine_workspace_size": ([_I64], _SZ),
     "exq_combine": ([_P, _INT, _P, _I64, _P, _INT, _I64, _I64, _I64, _P, _P, _SZ, _P], _INT),
     "exq_silu_and_mul": ([_P, _INT, _I64, _I64, _P, _P], _INT),
-    "exq_moe_gemm_workspace_size": ([_I64, _I64], _SZ),
+    "exq_moe_gemm_workspace_size": ([_I64, _I64, _I64], _SZ),
     "exq_moe_int4_gemm": ([_P, _INT, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _P, _P, _SZ, _P], _INT),
     "exq_moe_grouped_gemm": ([_P, _INT, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _P, _SZ, _P], _INT),
     "exq_moe_workspace_size": ([C.POINTER(MoeProblem)], _SZ),

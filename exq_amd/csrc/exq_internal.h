@@ -6,9 +6,11 @@
 
 namespace exq {
 
-// Tokens of one expert are processed in groups of at most this many rows
-// (four 16-row MFMA tiles).
+// Tokens of one expert are processed in groups of at most this many rows:
+// four 16-row MFMA tiles for BF16 / INT8 experts, eight for INT4 experts
+// (the tiled prefill kernel's 128-row tile).
 constexpr int kTokenGroup = 64;
+constexpr int kTokenGroupI4 = 128;
 
 // One work item of the grouped kernels: rows [pos0, pos0 + cnt) of the
 // expert-sorted order, all routed to expert `e` whose precision tier is
@@ -26,6 +28,53 @@ inline int64_t tg_capacity(int64_t n_rows, int64_t n_buckets) {
   return a + cdiv(n_rows, kTokenGroup) + 1;
 }
 
+// Grouped-GEMM modes: gate/up + SiLU into `mid`, plain C = A x W^T, down
+// projection into fp32 partial rows per slot.
+enum Mode { MODE_GATEUP = 0, MODE_PLAIN = 1, MODE_DOWN = 2 };
+
+// Weights of one projection (w13 or w2) for every precision tier.
+struct Bank {
+  const int8_t* tier;     // per-expert tier or null (all INT4)
+  const int32_t* index;   // per-expert row in the tier bank or null (identity)
+  const uint16_t* bf16;   // [nb, rows, K] activation dtype
+  const int8_t* i8;       // [n8, rows, K]
+  const uint16_t* i8_scales;  // [n8, rows]
+  const uint8_t* i4;      // [n4, rows, K/2]
+  const uint16_t* i4_scales;  // [n4, rows, K/g]
+};
+
+struct GemmArgs {
+  const int* hdr;          // hdr[0] = number of token groups, hdr[1] = first INT4 group
+  const TgEntry* tg;
+  int n_blocks;            // row blocks per token group
+  const uint16_t* x;       // activations (f16/bf16 bits)
+  int64_t x_stride;        // elements per activation row
+  const int* row_slot;     // expert-sorted position -> slot (GATEUP input, DOWN output)
+  int slot_div;            // slots per token (kp)
+  int K;                   // contraction length, multiple of 128
+  Bank w;
+  int n_rows;              // weight rows per expert
+  int inter;               // I: offset of the up rows (GATEUP)
+  int group_size;          // INT4 group size, multiple of 128
+  void* out;               // GATEUP mid [n, I] act | PLAIN C [rows, N] act | DOWN partial [n, H] f32
+  int64_t out_stride;
+  int H;
+  int skip_i4;             // INT4 token groups belong to the tiled kernel: skip them
+};
+
+// Tiled prefill GEMM (prefill.hip) over the INT4 token groups of the plan,
+// entries [hdr[1], hdr[0]) of the token-group list (cnt <= kTokenGroupI4):
+// work-group tile = 128 expert-sorted rows x 128 weight rows.  It needs
+// the per-row group sums of its activations, scaled by the nibble base,
+// from launch_group_rowsum (rs [K / group_size][rs_rows]; GATEUP rows are
+// tokens, DOWN / PLAIN rows are expert-sorted positions).
+bool tile_gemm_applies(int mode, int n_rows, int inter, int K, int group_size);
+int64_t tile_rowsum_floats(int64_t rows, int64_t K);  // rs floats for any group size
+int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows, int K, int gs,
+                        float* out, hipStream_t s);
+int launch_tile_gemm(int mode, bool bf, const GemmArgs& a, const float* rs, int64_t rs_rows,
+                     int64_t x_bytes, int64_t tg_cap, hipStream_t s);
+
 // Parameters of the routing-plan kernel (one work-group).
 struct RoutePlanParams {
   const void* ids;
@@ -33,11 +82,12 @@ struct RoutePlanParams {
   int T, k, kp, E, Ep;  // kp = k + n_shared, Ep = E + n_shared
   int n;                // T * kp
   const int8_t* tier;   // [Ep] or null (all INT4)
-  int* hdr;             // hdr[0] = number of token groups
+  int* hdr;             // hdr[0] = number of token groups, hdr[1] = first INT4 group
   int* ends;            // [Ep + 1]
   int* sorted;          // [n] slot ids in expert-sorted order
   TgEntry* tg;          // [tg_cap]
   int tg_cap;
+  int i4_group;         // rows per INT4 token group (kTokenGroup or kTokenGroupI4)
   int* counters;        // combine arrival counters, zeroed here
   int n_counters;
   int64_t* sort_order_out;  // optional [T*k]
@@ -50,7 +100,7 @@ int launch_route_plan(const RoutePlanParams& p, hipStream_t stream);
 
 // Token groups from user-provided expert boundaries (sorted-row GEMM API).
 int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, int tier,
-                        int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream);
+                        int group, int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream);
 
 // One-launch decode layer (decode.hip): routing, gate/up + SiLU, down and the
 // combine in a single persistent kernel.  `sync` points at the zero-filled

@@ -29,36 +29,6 @@ constexpr int WAVE_LDS = 18432;      // LDS bytes per wave
 constexpr int XS_OFF = 17408;        // offset of the row-sum area inside a wave's LDS
 constexpr int WG_LDS = NW * WAVE_LDS;
 
-enum Mode { MODE_GATEUP = 0, MODE_PLAIN = 1, MODE_DOWN = 2 };
-
-// Weights of one projection (w13 or w2) for every precision tier.
-struct Bank {
-  const int8_t* tier;     // per-expert tier or null (all INT4)
-  const int32_t* index;   // per-expert row in the tier bank or null (identity)
-  const uint16_t* bf16;   // [nb, rows, K] activation dtype
-  const int8_t* i8;       // [n8, rows, K]
-  const uint16_t* i8_scales;  // [n8, rows]
-  const uint8_t* i4;      // [n4, rows, K/2]
-  const uint16_t* i4_scales;  // [n4, rows, K/g]
-};
-
-struct GemmArgs {
-  const int* hdr;          // hdr[0] = number of token groups
-  const TgEntry* tg;
-  int n_blocks;            // row blocks per token group
-  const uint16_t* x;       // activations (f16/bf16 bits)
-  int64_t x_stride;        // elements per activation row
-  const int* row_slot;     // expert-sorted position -> slot (GATEUP input, DOWN output)
-  int slot_div;            // slots per token (kp)
-  int K;                   // contraction length, multiple of 128
-  Bank w;
-  int n_rows;              // weight rows per expert
-  int inter;               // I: offset of the up rows (GATEUP)
-  int group_size;          // INT4 group size, multiple of 128
-  void* out;               // GATEUP mid [n, I] act | PLAIN C [rows, N] act | DOWN partial [n, H] f32
-  int64_t out_stride;
-  int H;
-};
 
 template <bool BF>
 __device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, f32x4_t c) {
@@ -390,7 +360,8 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TgEntry& te, 
 template <bool BF, int MODE>
 __global__ void __launch_bounds__(NTH, 2) moe_gemm_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[WG_LDS];
-  const int n_tg = a.hdr[0];
+  // INT4 token groups (the tail of the list) go to the tiled kernel when it runs.
+  const int n_tg = a.skip_i4 ? a.hdr[1] : a.hdr[0];
   const int U = n_tg * a.n_blocks;
   // XCD-aware order: work-group i runs on XCD i % 8, so each XCD takes a
   // contiguous range of units and neighbouring blocks of one token group
@@ -480,7 +451,7 @@ namespace {
 
 // ---- workspace layout of the fused forward --------------------------------------
 struct FusedLayout {
-  size_t sync, hdr, ends, sorted, tg, mid, partial, total;
+  size_t sync, hdr, ends, sorted, tg, mid, partial, rs, total;
   int64_t n, tg_cap;
 };
 
@@ -501,6 +472,10 @@ FusedLayout fused_layout(const exq_moe_problem& p) {
   L.tg = off;       off = align_up(off + (size_t)L.tg_cap * sizeof(TgEntry), 256);
   L.mid = off;      off = align_up(off + (size_t)L.n * p.inter_size * 2, 256);
   L.partial = off;  off = align_up(off + (size_t)L.n * p.hidden_size * 4, 256);
+  // group row sums of the tiled prefill kernel: x rows (GATEUP), then mid rows (DOWN)
+  const int64_t rs_x = tile_rowsum_floats(p.n_tokens, p.hidden_size);
+  const int64_t rs_mid = tile_rowsum_floats(L.n, p.inter_size);
+  L.rs = off;       off = align_up(off + (size_t)(rs_x > rs_mid ? rs_x : rs_mid) * 4, 256);
   L.total = off;
   return L;
 }
@@ -565,6 +540,14 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   rp.sorted = reinterpret_cast<int*>(ws + L.sorted);
   rp.tg = reinterpret_cast<TgEntry*>(ws + L.tg);
   rp.tg_cap = (int)L.tg_cap;
+  // INT4 experts run on the tiled kernel (128-row token groups) when both
+  // projections fit it and the gathered activations are 32-bit addressable.
+  const int gs = (int)p->group_size;
+  const bool tile = tile_gemm_applies(MODE_GATEUP, 2 * I, I, H, gs) &&
+                    tile_gemm_applies(MODE_DOWN, H, I, I, gs) &&
+                    (int64_t)T * H * 2 <= 0x7fffffffLL &&
+                    tile_rowsum_floats(L.n, I) * 4 <= 0x7fffffffLL;
+  rp.i4_group = tile ? kTokenGroupI4 : kTokenGroup;
   rp.counters = nullptr;
   rp.n_counters = 0;
   rp.sort_order_out = sort_order_out;
@@ -619,8 +602,12 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     g.tg = rp.tg;
     g.row_slot = rp.sorted;
     g.slot_div = kp;
-    g.group_size = (int)p->group_size;
+    g.group_size = gs;
     g.inter = I;
+    g.skip_i4 = tile ? 1 : 0;
+    // Without a tier array every expert is INT4: the tiled kernel does it all.
+    const bool old_kernel = !tile || tier != nullptr;
+    float* rs = reinterpret_cast<float*>(ws + L.rs);
     // gate/up + SiLU: x = hidden, K = H, rows = 2I, out = mid [n, I] (sorted rows)
     g.n_blocks = I / 16;
     g.x = reinterpret_cast<const uint16_t*>(hidden);
@@ -630,8 +617,16 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     g.n_rows = 2 * I;
     g.out = ws + L.mid;
     g.out_stride = I;
-    st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
-    if (st) return st;
+    if (old_kernel) {
+      st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
+      if (st) return st;
+    }
+    if (tile) {
+      st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
+      if (st) return st;
+      st = launch_tile_gemm(MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s);
+      if (st) return st;
+    }
     st = record_stage(2, s);
     if (st) return st;
     // down: x = mid rows (expert-sorted), K = I, rows = H, out = partial [slot, H]
@@ -644,8 +639,16 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     g.out = ws + L.partial;
     g.out_stride = H;
     g.H = H;
-    st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
-    if (st) return st;
+    if (old_kernel) {
+      st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
+      if (st) return st;
+    }
+    if (tile) {
+      st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
+      if (st) return st;
+      st = launch_tile_gemm(MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s);
+      if (st) return st;
+    }
   }
   const int64_t threads = (int64_t)T * (H / 4);
   if (bf)
@@ -679,7 +682,9 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
                           "%s: group_size=%lld must be a multiple of 128 dividing K", fn,
                           (long long)gs);
   const int64_t tg_cap = tg_capacity(n_rows, n_experts);
-  const size_t need = align_up(64, 256) + align_up((size_t)tg_cap * sizeof(TgEntry), 256);
+  const size_t tg_off = align_up(64, 256);
+  const size_t rs_off = tg_off + align_up((size_t)tg_cap * sizeof(TgEntry), 256);
+  const size_t need = rs_off + align_up((size_t)tile_rowsum_floats(n_rows, K) * 4, 256);
   if (n_rows == 0) return EXQ_SUCCESS;
   if (workspace_bytes < need)
     return set_error(EXQ_ERROR_WORKSPACE_TOO_SMALL, "%s: workspace %zu < %zu bytes", fn,
@@ -689,8 +694,12 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
               "%s: A and workspace must be 16-byte aligned", fn);
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
   int* hdr = reinterpret_cast<int*>(ws);
-  TgEntry* tg = reinterpret_cast<TgEntry*>(ws + align_up(64, 256));
-  int st = launch_tg_from_ends(ends, (int)n_experts, mask, tier, hdr, tg, (int)tg_cap, s);
+  TgEntry* tg = reinterpret_cast<TgEntry*>(ws + tg_off);
+  const bool bf = act_dtype == EXQ_DTYPE_BF16;
+  const bool tile = tier == 2 && tile_gemm_applies(MODE_PLAIN, (int)N, 0, (int)K, (int)gs) &&
+                    tile_rowsum_floats(n_rows, K) * 4 <= 0x7fffffffLL;
+  int st = launch_tg_from_ends(ends, (int)n_experts, mask, tier,
+                               tile ? kTokenGroupI4 : kTokenGroup, hdr, tg, (int)tg_cap, s);
   if (st) return st;
   GemmArgs g{};
   g.hdr = hdr;
@@ -704,7 +713,13 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
   g.group_size = (int)gs;
   g.out = c;
   g.out_stride = N;
-  return launch_gemm<MODE_PLAIN>(act_dtype == EXQ_DTYPE_BF16, g, tg_cap * g.n_blocks, s);
+  if (tile) {
+    float* rs = reinterpret_cast<float*>(ws + rs_off);
+    st = launch_group_rowsum(bf, g.x, K, n_rows, (int)K, (int)gs, rs, s);
+    if (st) return st;
+    return launch_tile_gemm(MODE_PLAIN, bf, g, rs, n_rows, 0, tg_cap, s);
+  }
+  return launch_gemm<MODE_PLAIN>(bf, g, tg_cap * g.n_blocks, s);
 }
 
 }  // namespace
@@ -731,9 +746,10 @@ extern "C" int exq_set_stage_events(void* const* events, int n_events) {
   return EXQ_SUCCESS;
 }
 
-extern "C" size_t exq_moe_gemm_workspace_size(int64_t n_rows, int64_t n_experts) {
-  return align_up(64, 256) +
-         align_up((size_t)tg_capacity(n_rows > 0 ? n_rows : 0, n_experts) * sizeof(TgEntry), 256);
+extern "C" size_t exq_moe_gemm_workspace_size(int64_t n_rows, int64_t n_experts, int64_t K) {
+  const int64_t r = n_rows > 0 ? n_rows : 0;
+  return align_up(64, 256) + align_up((size_t)tg_capacity(r, n_experts) * sizeof(TgEntry), 256) +
+         align_up((size_t)tile_rowsum_floats(r, K > 0 ? K : 0) * 4, 256);
 }
 
 extern "C" int exq_moe_int4_fused_forward(const exq_moe_problem* problem, const void* hidden,

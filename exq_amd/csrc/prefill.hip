@@ -1,0 +1,475 @@
+// prefill.hip -- tiled grouped GEMM for INT4 experts on gfx950 MFMA (the
+// prefill / large-batch path of the fused layer and of exq_moe_int4_gemm).
+//
+// Work decomposition.  One work-group computes a 128 x 128 output tile: the
+// <= 128 expert-sorted rows of one token group (one expert) times 128 weight
+// rows of that expert:
+//   GATEUP: 64 gate rows j0..j0+63 and the matching up rows I+j0.., SiLU(g)*u
+//           written to `mid` (each wave holds gate and up columns of the same j,
+//           so the product is lane-local);
+//   DOWN / PLAIN: 128 consecutive weight rows.
+// Four waves split the tile (2 x 2 of 64 x 64, or 1 x 4 of 128 x 32); each
+// wave owns its sub-tile over the whole contraction, so no cross-wave
+// reduction is needed.
+//
+// Data movement.  The contraction runs in chunks of 128 k (one fp16 scale
+// group step).  A chunk of activations (128 rows x 256 B, gathered rows for
+// GATEUP) and of packed weights (128 rows x 64 B) is copied straight from
+// global memory into LDS by buffer_load ... lds (16 B per lane, 64 lanes per
+// 1 KiB instruction), double-buffered: chunk c+1 is in flight while chunk c
+// is multiplied.  Both LDS images are XOR-swizzled in 16-byte columns so the
+// MFMA operand reads (16 rows, one column) hit distinct banks.
+//
+// Arithmetic.  Lane (r, q) of an MFMA 16x16x32 operand holds 8 k values; the
+// k assignment is chosen so that a lane's B values for the whole chunk are 16
+// consecutive packed bytes (k = 32q + 8s + i at k-step s): one ds_read_b128
+// per weight tile and chunk, and the A fragment for step s is 16 consecutive
+// bytes of the staged row.  Nibbles become exact 16-bit floats 128+n (bf16)
+// or 1024+n (f16) in natural k order with one v_perm_b32 and one
+// v_and_or_b32 per pair; the constant base (136 / 1032) times the row's group
+// sum -- precomputed by group_rowsum_kernel -- is the MFMA accumulator's
+// starting value, so each group's sum is exact before the fp16 group scale
+// multiplies it in fp32.
+#include "exq_internal.h"
+
+namespace exq {
+namespace {
+
+constexpr int TT = 256;              // threads per work-group (4 waves)
+constexpr int TM = 128;              // expert-sorted rows per tile
+constexpr int KC = 128;              // contraction per chunk
+constexpr int A_STAGE = TM * KC * 2; // 32 KiB of activations per chunk
+constexpr int B_STAGE = 128 * KC / 2;  // 8 KiB of packed weights per chunk
+
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+// 16 bytes per lane from buffer `r` at byte offset voff + soff into LDS at
+// lds + 16 * lane (buffer_load_dwordx4 ... lds); `lds` and `soff` are
+// wave-uniform.  The builtin exists only for the device target.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff,
+                                      int soff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)lds, 16, voff, soff, 0, 0);
+#endif
+}
+
+// Buffer resource over `bytes` bytes at `base`: loads beyond the range return
+// zero without a memory access (a zero-length resource never touches memory).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int n = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+// Waits written as volatile asm with a memory clobber so that no LDS access
+// moves across them: LDS written by buffer_load ... lds is ordered only by the
+// vmcnt wait, which the compiler does not model as a dependency of LDS reads.
+__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Every wave's chunk has landed and every wave has finished reading the other
+// stage.  (__syncthreads would add a release fence that also waits for the
+// prefetch just issued.)
+__device__ __forceinline__ void chunk_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <bool BF>
+__device__ __forceinline__ f32x4_t mfma16(const uint4& a, const uint4& b, f32x4_t c) {
+  if constexpr (BF) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// 8 packed nibbles (k offsets 0..7, low nibble = even k) -> 8 exact 16-bit
+// floats (base + nibble) in natural k order.  Pair j takes byte j of p (low
+// nibble, k = 2j) and byte j of p >> 4 (its low nibble is k = 2j + 1).
+__device__ __forceinline__ uint4 deq_nat(uint32_t p, uint32_t mask, uint32_t magic) {
+  const uint32_t h = p >> 4;
+  uint4 o;
+  o.x = (__builtin_amdgcn_perm(h, p, 0x0c040c00u) & mask) | magic;
+  o.y = (__builtin_amdgcn_perm(h, p, 0x0c050c01u) & mask) | magic;
+  o.z = (__builtin_amdgcn_perm(h, p, 0x0c060c02u) & mask) | magic;
+  o.w = (__builtin_amdgcn_perm(h, p, 0x0c070c03u) & mask) | magic;
+  return o;
+}
+
+// Lane n of each 16-lane row, broadcast to the whole row (DPP row_newbcast).
+// `n` is a constant after unrolling; the switch folds away.
+template <int N>
+__device__ __forceinline__ float row_bcast_n(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + N, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row_bcast(float v, int n) {
+  switch (n) {
+    case 0: return row_bcast_n<0>(v);
+    case 1: return row_bcast_n<1>(v);
+    case 2: return row_bcast_n<2>(v);
+    case 3: return row_bcast_n<3>(v);
+    case 4: return row_bcast_n<4>(v);
+    case 5: return row_bcast_n<5>(v);
+    case 6: return row_bcast_n<6>(v);
+    case 7: return row_bcast_n<7>(v);
+    case 8: return row_bcast_n<8>(v);
+    case 9: return row_bcast_n<9>(v);
+    case 10: return row_bcast_n<10>(v);
+    case 11: return row_bcast_n<11>(v);
+    case 12: return row_bcast_n<12>(v);
+    case 13: return row_bcast_n<13>(v);
+    case 14: return row_bcast_n<14>(v);
+    default: return row_bcast_n<15>(v);
+  }
+}
+
+template <bool BF>
+__device__ __forceinline__ uint32_t to_act_bits(float v) {
+  return BF ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
+}
+
+// Swizzle of the 16-byte column c of LDS weight row r (4 columns per 64-byte
+// row): conflict-free ds_read_b128 for 16 consecutive rows at one column
+// whether the LDS serves 8 or 16 lanes per cycle.
+__device__ __forceinline__ int b_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+struct TileArgs {
+  const float* rs;   // [K / group_size][rs_rows]: base * (row sum over the group)
+  int rs_rows;
+  int64_t x_bytes;   // bytes addressable from a.x (GATEUP gather)
+  int n_tiles;       // weight tiles per expert (I / 64 for GATEUP, rows / 128 otherwise)
+};
+
+// MT = m-tiles (16 rows) per wave: 4 -> waves 2 x 2 of 64 x 64; 8 -> 1 x 4 of 128 x 32.
+template <bool BF, int MODE, int MT>
+__global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs ta) {
+  constexpr int WAVES_M = 8 / MT;
+  constexpr int WAVES_N = 4 / WAVES_M;
+  constexpr int NTW = 8 / WAVES_N;  // n-tiles (16 weight rows) per wave
+  constexpr int HALF = NTW / 2;
+  constexpr int RSR = MT / 4;       // row sums held per lane (64 rows each)
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[A_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[B_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[B_STAGE];
+
+  // ---- unit: (token group, weight tile), XCD-aware order -------------------
+  // Work-group i runs on XCD i % 8 and each XCD takes a contiguous range of
+  // units; inside it, 64 consecutive units are 8 token groups x 8 weight
+  // tiles, so concurrently running tiles share activation and weight chunks
+  // in that XCD's L2.
+  const int t0 = a.hdr[1];
+  const int n4 = a.hdr[0] - t0;
+  const int NT = ta.n_tiles;
+  const int U = ((n4 + 7) >> 3) * 8 * NT;
+  const int per = (U + 7) >> 3;
+  const int local = blockIdx.x >> 3;
+  const int v = (blockIdx.x & 7) * per + local;
+  if (local >= per || v >= U) return;
+  const int tb = v / (8 * NT);
+  const int rem = v - tb * 8 * NT;
+  const int nt = rem >> 3;
+  const int tgi = tb * 8 + (rem & 7);
+  if (tgi >= n4) return;
+  const TgEntry te = a.tg[t0 + tgi];
+  const int cnt = te.cnt, pos0 = te.pos0;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS DMA bases in SGPRs
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int K = a.K;
+  const int nch = K / KC;
+  const int ngs = K / KC;  // scale groups (group_size == KC)
+
+  const int widx = a.w.index ? a.w.index[te.e] : te.e;
+  const int64_t ebase = (int64_t)widx * a.n_rows;
+  const int rowbytes = K / 2;
+  auto wrow = [&](int rho) -> int {  // weight row (within the expert) of LDS row rho
+    if constexpr (MODE == MODE_GATEUP)
+      return rho < 64 ? nt * 64 + rho : a.inter + nt * 64 + (rho - 64);
+    else
+      return nt * 128 + rho;
+  };
+  auto brow = [&](int t) -> int {  // first LDS weight row of this wave's n-tile t
+    if constexpr (MODE == MODE_GATEUP)
+      return t < HALF ? wn * HALF * 16 + t * 16 : 64 + wn * HALF * 16 + (t - HALF) * 16;
+    else
+      return wn * NTW * 16 + t * 16;
+  };
+  // Row m (0..127) of the tile: rows past the group repeat its last row
+  // (finite values whose outputs are never stored).
+  auto x_row = [&](int m) -> int {  // activation row (GATEUP: token) of tile row m
+    const int mm = m < cnt ? m : cnt - 1;
+    if constexpr (MODE == MODE_GATEUP)
+      return a.row_slot[pos0 + mm] / a.slot_div;
+    else
+      return pos0 + mm;
+  };
+
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(a.w.i4 + ebase * rowbytes, (int64_t)a.n_rows * rowbytes);
+  const __amdgpu_buffer_rsrc_t sr =
+      make_rsrc(a.w.i4_scales + ebase * ngs, (int64_t)a.n_rows * ngs * 2);
+  const __amdgpu_buffer_rsrc_t xr =
+      MODE == MODE_GATEUP
+          ? make_rsrc(a.x, ta.x_bytes)
+          : make_rsrc(a.x + (int64_t)pos0 * a.x_stride, (int64_t)cnt * a.x_stride * 2);
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(ta.rs, (int64_t)ngs * ta.rs_rows * 4);
+  const __amdgpu_buffer_rsrc_t wnull = make_rsrc(a.w.i4, 0);
+  const __amdgpu_buffer_rsrc_t snull = make_rsrc(a.w.i4_scales, 0);
+  const __amdgpu_buffer_rsrc_t xnull = make_rsrc(a.x, 0);
+  const __amdgpu_buffer_rsrc_t rnull = make_rsrc(ta.rs, 0);
+
+  // ---- per-lane DMA offsets ------------------------------------------------
+  int voffA[8], voffB[2];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {  // LDS rows 4j..4j+3 per instruction, 16 columns each
+    const int m = (wave * 8 + q) * 4 + (lane >> 4);
+    const int c = (lane & 15) ^ (m & 15);
+    const int xrow = x_row(m);
+    voffA[q] = (MODE == MODE_GATEUP ? xrow : xrow - pos0) * (int)a.x_stride * 2 + c * 16;
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {  // LDS rows 16j..16j+15 per instruction, 4 columns each
+    const int rho = (wave * 2 + q) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ b_swz(rho & 15);
+    voffB[q] = wrow(rho) * rowbytes + c * 16;
+  }
+  // Scale of weight row wrow(brow(t) + r16): lane part + a wave-uniform delta.
+  const int soffS = wrow(brow(0) + r16) * ngs * 2;
+  int sdel[NTW];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t)
+    sdel[t] = __builtin_amdgcn_readfirstlane((wrow(brow(t) + r16) - wrow(brow(0) + r16)) * ngs * 2);
+  // Row sums: lane kq*16 + n holds tile row (n >> 2) * 16 + kq * 4 + (n & 3)
+  // (+ 64 per register), so that the accumulator start of m-tile mt, element
+  // v, is lane mt*4 + v of the lane's own 16-lane row (DPP row_newbcast).
+  int soffR[RSR];
+#pragma unroll
+  for (int i = 0; i < RSR; ++i)
+    soffR[i] = x_row(wm * MT * 16 + i * 64 + (r16 >> 2) * 16 + kq * 4 + (r16 & 3)) * 4;
+
+  // LDS read offsets: A fragment of k-step s = aoff ^ (16 s) (+ 4 KiB per
+  // m-tile); weight tile t = boff + bdel(t).
+  const int aoff = (wm * MT * 16 + r16) * 256 + (((kq * 4) ^ r16) * 16);
+  const int boff = (brow(0) + r16) * 64 + ((kq ^ b_swz(r16)) * 16);
+  uint32_t sc_raw[2][NTW];
+  float rs_raw[2][RSR];
+
+  auto prefetch = [&](int st, int ch) {
+    const bool ok = ch < nch;
+    const int chl = ok ? ch : 0;
+    const int g = chl;
+    unsigned char* A = st ? sA1 : sA0;
+    unsigned char* B = st ? sB1 : sB0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) dma16(ok ? xr : xnull, A + (wave * 8 + q) * 1024, voffA[q], chl * 256);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) dma16(ok ? wr : wnull, B + (wave * 2 + q) * 1024, voffB[q], chl * 64);
+#pragma unroll
+    for (int t = 0; t < NTW; ++t)
+      sc_raw[st][t] =
+          __builtin_amdgcn_raw_buffer_load_b16(ok ? sr : snull, soffS, g * 2 + sdel[t], 0);
+#pragma unroll
+    for (int i = 0; i < RSR; ++i)
+      rs_raw[st][i] = __builtin_bit_cast(
+          float, __builtin_amdgcn_raw_buffer_load_b32(ok ? rr : rnull, soffR[i], g * ta.rs_rows * 4, 0));
+  };
+
+  const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(dq_magic));  // magic in a VGPR: one v_and_or_b32 per pair
+
+  f32x4_t tot[MT][NTW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) tot[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#define EXQ_TILE_CHUNK(ST, FIRST, LAST)                                                      \
+  do {                                                                                       \
+    const unsigned char* A_ = ST ? sA1 : sA0;                                                \
+    const unsigned char* B_ = ST ? sB1 : sB0;                                                \
+    f32x4_t acc[MT][NTW];                                                                    \
+    uint4 bw[NTW];                                                                           \
+    _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                          \
+        bw[t] = *reinterpret_cast<const uint4*>(B_ + boff + (brow(t) - brow(0)) * 64);      \
+    f32x4_t cin[MT];                                                                         \
+    if (FIRST) {                                                                             \
+      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
+          _Pragma("unroll") for (int v_ = 0; v_ < 4; ++v_)                                   \
+              cin[mt][v_] = row_bcast(rs_raw[ST][mt >> 2], (mt & 3) * 4 + v_);               \
+    }                                                                                        \
+    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                                          \
+      uint4 af[MT];                                                                          \
+      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
+          af[mt] = *reinterpret_cast<const uint4*>(A_ + (aoff ^ (s * 16)) + mt * 16 * 256);  \
+      uint4 bf[NTW];                                                                         \
+      _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                      \
+        const uint32_t p_ = s == 0 ? bw[t].x : s == 1 ? bw[t].y : s == 2 ? bw[t].z : bw[t].w; \
+        bf[t] = deq_nat(p_, dq_mask, dq_magic);                                              \
+      }                                                                                      \
+      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
+          _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                    \
+              acc[mt][t] = mfma16<BF>(af[mt], bf[t], (FIRST && s == 0) ? cin[mt] : acc[mt][t]); \
+    }                                                                                        \
+    if (LAST) {                                                                              \
+      _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                      \
+        const float sc_ = f16_bits_to_f32(sc_raw[ST][t]);                                    \
+        _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) tot[mt][t] += sc_ * acc[mt][t];    \
+      }                                                                                      \
+    }                                                                                        \
+  } while (0)
+
+  // One chunk is one scale group (group_size 128): each chunk's sums start
+  // from the base correction and end scaled into tot.
+  // The scheduling barriers keep each prefetch at the head of its chunk (the
+  // scheduler would otherwise sink the loads into the MFMA stream).
+  prefetch(0, 0);
+  for (int ch = 0; ch < nch; ch += 2) {
+    chunk_barrier();
+    prefetch(1, ch + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    EXQ_TILE_CHUNK(0, true, true);
+    if (ch + 1 >= nch) break;
+    chunk_barrier();
+    prefetch(0, ch + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    EXQ_TILE_CHUNK(1, true, true);
+  }
+#undef EXQ_TILE_CHUNK
+  wait_vm_all();  // the last (empty) prefetch has drained before the work-group ends
+
+  // ---- epilogue --------------------------------------------------------------
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int v_ = 0; v_ < 4; ++v_) {
+      const int m = wm * MT * 16 + mt * 16 + kq * 4 + v_;
+      if (m >= cnt) continue;
+      const int pos = pos0 + m;
+      if constexpr (MODE == MODE_GATEUP) {
+        uint16_t* mid = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
+                        nt * 64 + wn * HALF * 16 + r16;
+#pragma unroll
+        for (int t = 0; t < HALF; ++t)
+          mid[t * 16] = (uint16_t)to_act_bits<BF>(silu_f32(tot[mt][t][v_]) * tot[mt][t + HALF][v_]);
+      } else if constexpr (MODE == MODE_PLAIN) {
+        uint16_t* c = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
+                      nt * 128 + wn * NTW * 16 + r16;
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) c[t * 16] = (uint16_t)to_act_bits<BF>(tot[mt][t][v_]);
+      } else {
+        const int slot = a.row_slot[pos];
+        float* part = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.out_stride + nt * 128 +
+                      wn * NTW * 16 + r16;
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) part[t * 16] = tot[mt][t][v_];
+      }
+    }
+  }
+}
+
+// out[g][r] = base * sum_{k in group g} x[r, k] (fp32 sums of the 16-bit
+// values) for base = -136 (bf16) or -1032 (f16): the accumulator start of the
+// tiled kernel.  One work-group per row; 16 lanes cover one 128-element block.
+template <bool BF>
+__global__ void __launch_bounds__(256) group_rowsum_kernel(const uint16_t* __restrict__ x,
+                                                           int64_t stride, int R, int K, int gs,
+                                                           float base, float* __restrict__ out) {
+  __shared__ float bs[512];
+  const int r = blockIdx.x;
+  const uint16_t* row = x + (int64_t)r * stride;
+  const int np = K / 8;  // 16-byte pieces, a multiple of 16
+  for (int p0 = 0; p0 < np; p0 += 256) {
+    const int p = p0 + (int)threadIdx.x;
+    float s = 0.f;
+    if (p < np) {
+      const uint4 v = *reinterpret_cast<const uint4*>(row + (int64_t)p * 8);
+      const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (BF)
+          s += __uint_as_float(d[i] << 16) + __uint_as_float(d[i] & 0xffff0000u);
+        else
+          s += f16_bits_to_f32(d[i] & 0xffffu) + f16_bits_to_f32(d[i] >> 16);
+      }
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    s += __shfl_xor(s, 4, 64);
+    s += __shfl_xor(s, 8, 64);
+    if (p < np && (threadIdx.x & 15) == 0) bs[p >> 4] = s;
+  }
+  __syncthreads();
+  const int ng = K / gs, nb = gs / 128;
+  for (int g = threadIdx.x; g < ng; g += 256) {
+    float s = 0.f;
+    for (int i = 0; i < nb; ++i) s += bs[g * nb + i];
+    out[(int64_t)g * R + r] = base * s;
+  }
+}
+
+}  // namespace
+
+bool tile_gemm_applies(int mode, int n_rows, int inter, int K, int group_size) {
+  if (K < KC || K % KC != 0 || K > 65536) return false;
+  if (group_size != KC) return false;  // one chunk = one scale group
+  if (mode == MODE_GATEUP) {
+    if (inter % 64 != 0 || n_rows != 2 * inter) return false;
+  } else if (n_rows % 128 != 0) {
+    return false;
+  }
+  // 32-bit buffer offsets within one expert's weights and scales
+  if ((int64_t)n_rows * (K / 2) > 0x7fffffffLL) return false;
+  return true;
+}
+
+int64_t tile_rowsum_floats(int64_t rows, int64_t K) { return rows * (K / KC); }
+
+int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows, int K, int gs,
+                        float* out, hipStream_t s) {
+  if (rows <= 0) return EXQ_SUCCESS;
+  if (rows > INT32_MAX) return set_error(EXQ_ERROR_UNSUPPORTED, "group_rowsum: too many rows");
+  if (bf)
+    hipLaunchKernelGGL(group_rowsum_kernel<true>, dim3((unsigned)rows), dim3(256), 0, s, x, stride,
+                       (int)rows, K, gs, -136.0f, out);
+  else
+    hipLaunchKernelGGL(group_rowsum_kernel<false>, dim3((unsigned)rows), dim3(256), 0, s, x,
+                       stride, (int)rows, K, gs, -1032.0f, out);
+  return check_launch("group_rowsum_kernel");
+}
+
+template <int MODE>
+static int launch_tile_mode(bool bf, const GemmArgs& a, const TileArgs& t, int64_t grid,
+                            hipStream_t s) {
+  if (bf)
+    hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 4>), dim3((unsigned)grid), dim3(TT), 0, s, a,
+                       t);
+  else
+    hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 4>), dim3((unsigned)grid), dim3(TT), 0, s,
+                       a, t);
+  return check_launch("tile_gemm_kernel");
+}
+
+int launch_tile_gemm(int mode, bool bf, const GemmArgs& a, const float* rs, int64_t rs_rows,
+                     int64_t x_bytes, int64_t tg_cap, hipStream_t s) {
+  TileArgs t;
+  t.rs = rs;
+  t.rs_rows = (int)rs_rows;
+  t.x_bytes = x_bytes;
+  t.n_tiles = mode == MODE_GATEUP ? a.inter / 64 : a.n_rows / 128;
+  const int64_t grid = 8 * cdiv(tg_cap, 8) * t.n_tiles;
+  if (grid <= 0) return EXQ_SUCCESS;
+  if (grid > INT32_MAX || rs_rows > INT32_MAX)
+    return set_error(EXQ_ERROR_UNSUPPORTED, "tile_gemm: problem too large");
+  if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(bf, a, t, grid, s);
+  if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(bf, a, t, grid, s);
+  return launch_tile_mode<MODE_PLAIN>(bf, a, t, grid, s);
+}
+
+}  // namespace exq

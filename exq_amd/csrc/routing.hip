@@ -233,10 +233,12 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
 
   // Token groups, heaviest tier first so long work items start early.
   const int c = b < nb ? s.cnt[b] : 0;
-  const int ng = (c + kTokenGroup - 1) / kTokenGroup;
   const int my_tier = (b < nb) ? (p.tier ? (int)p.tier[b] : 2) : -1;
-  int base = 0;
+  const int gsz = my_tier == 2 ? p.i4_group : kTokenGroup;
+  const int ng = (c + gsz - 1) / gsz;
+  int base = 0, first_i4 = 0;
   for (int tr = (p.tier ? 0 : 2); tr <= 2; ++tr) {
+    if (tr == 2) first_i4 = base;
     int tot;
     int off = block_excl_scan(my_tier == tr ? ng : 0, s.wsum, &tot);
     if (my_tier == tr) {
@@ -245,8 +247,8 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
         if (slot < p.tg_cap) {
           TgEntry te;
           te.e = b;
-          te.pos0 = s.start[b] + g * kTokenGroup;
-          te.cnt = min(kTokenGroup, c - g * kTokenGroup);
+          te.pos0 = s.start[b] + g * gsz;
+          te.cnt = min(gsz, c - g * gsz);
           te.tier = tr;
           p.tg[slot] = te;
         }
@@ -254,7 +256,10 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
     }
     base += tot;
   }
-  if (threadIdx.x == 0) p.hdr[0] = base < p.tg_cap ? base : p.tg_cap;
+  if (threadIdx.x == 0) {
+    p.hdr[0] = base < p.tg_cap ? base : p.tg_cap;
+    p.hdr[1] = first_i4 < p.tg_cap ? first_i4 : p.tg_cap;
+  }
   for (int i = threadIdx.x; i < p.n_counters; i += RT) p.counters[i] = 0;
   if (base == 0 && p.out) {
     uint32_t* o = reinterpret_cast<uint32_t*>(p.out);
@@ -265,7 +270,8 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
 // ---- token groups from user boundaries ------------------------------------------
 __global__ void __launch_bounds__(RT) tg_from_ends_kernel(const int32_t* ends, int E,
                                                           const int32_t* mask, int tier,
-                                                          int* hdr, TgEntry* tg, int tg_cap) {
+                                                          int gsz, int* hdr, TgEntry* tg,
+                                                          int tg_cap) {
   __shared__ int wsum[RT_WAVES];
   int base = 0;
   for (int e0 = 0; e0 < E; e0 += RT) {
@@ -276,7 +282,7 @@ __global__ void __launch_bounds__(RT) tg_from_ends_kernel(const int32_t* ends, i
       c = ends[e + 1] - lo;
       if (c < 0) c = 0;
     }
-    const int ng = (c + kTokenGroup - 1) / kTokenGroup;
+    const int ng = (c + gsz - 1) / gsz;
     int tot;
     int off = block_excl_scan(ng, wsum, &tot);
     for (int g = 0; g < ng; ++g) {
@@ -284,15 +290,18 @@ __global__ void __launch_bounds__(RT) tg_from_ends_kernel(const int32_t* ends, i
       if (slot < tg_cap) {
         TgEntry te;
         te.e = e;
-        te.pos0 = lo + g * kTokenGroup;
-        te.cnt = min(kTokenGroup, c - g * kTokenGroup);
+        te.pos0 = lo + g * gsz;
+        te.cnt = min(gsz, c - g * gsz);
         te.tier = tier;
         tg[slot] = te;
       }
     }
     base += tot;
   }
-  if (threadIdx.x == 0) hdr[0] = base < tg_cap ? base : tg_cap;
+  if (threadIdx.x == 0) {
+    hdr[0] = base < tg_cap ? base : tg_cap;
+    hdr[1] = tier == 2 ? 0 : hdr[0];
+  }
 }
 
 }  // namespace
@@ -303,9 +312,9 @@ int launch_route_plan(const RoutePlanParams& p, hipStream_t stream) {
 }
 
 int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, int tier,
-                        int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream) {
+                        int group, int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream) {
   hipLaunchKernelGGL(tg_from_ends_kernel, dim3(1), dim3(RT), 0, stream, ends, E, expert_mask,
-                     tier, hdr, tg, tg_cap);
+                     tier, group, hdr, tg, tg_cap);
   return check_launch("tg_from_ends_kernel");
 }
 

@@ -65,7 +65,7 @@ def moe_grouped_gemm(hidden_states: torch.Tensor, expert_weights: torch.Tensor,
     gather_hidden(hidden_states.contiguous(), sort_order, a, top_k)
     out = torch.zeros(n_active, N, dtype=hidden_states.dtype, device=dev)
     L = _lib.lib()
-    ws = _lib.workspace(dev, L.exq_moe_gemm_workspace_size(n_active, n_experts))
+    ws = _lib.workspace(dev, L.exq_moe_gemm_workspace_size(n_active, n_experts, K))
     mask = None
     if expert_mask is not None:
         mask = expert_mask.to(torch.int32).contiguous()

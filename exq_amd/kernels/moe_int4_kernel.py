@@ -132,7 +132,7 @@ def moe_int4_forward(hidden_states: torch.Tensor, expert_packed: torch.Tensor,
     gather_hidden(hidden_states, sort_order, a, top_k)
     out = torch.empty(n_active, N, dtype=hidden_states.dtype, device=dev)
     L = _lib.lib()
-    ws = _lib.workspace(dev, L.exq_moe_gemm_workspace_size(n_active, n_experts))
+    ws = _lib.workspace(dev, L.exq_moe_gemm_workspace_size(n_active, n_experts, K))
     _lib.check(L.exq_moe_int4_gemm(
         a.data_ptr(), _lib.dtype_code(a.dtype), n_active, K, expert_packed.data_ptr(),
         expert_scales.data_ptr(), n_experts, N, gs, ends.data_ptr(), out.data_ptr(),

@@ -147,9 +147,11 @@ int exq_silu_and_mul(const void* input, int dtype, int64_t rows, int64_t inter,
  * applied in fp32).  Replaces the _moe_gemm_int4_kernel launch of
  * moe_int4_forward (exq/kernels/moe_int4_kernel.py:124-240, 303-326).
  * A and C: f16 | bf16 (same dtype).  Requires K % 128 == 0 and
- * group_size % 128 == 0, N % 32 == 0.
+ * group_size % 128 == 0, N % 32 == 0.  exq_moe_gemm_workspace_size covers
+ * the token-group list and, for INT4 weights with N % 128 == 0 (the tiled
+ * kernel), the per-row group sums of A (n_rows * K / 128 floats).
  */
-size_t exq_moe_gemm_workspace_size(int64_t n_rows, int64_t n_experts);
+size_t exq_moe_gemm_workspace_size(int64_t n_rows, int64_t n_experts, int64_t K);
 int exq_moe_int4_gemm(const void* a_sorted, int act_dtype, int64_t n_rows, int64_t K,
                       const uint8_t* packed, const uint16_t* scales, int64_t n_experts,
                       int64_t N, int64_t group_size, const int32_t* expert_ends,

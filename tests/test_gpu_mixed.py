@@ -81,7 +81,7 @@ def test_mixed_olmoe_shape(device):
     assert E == bank.n_experts
 
 
-@pytest.mark.parametrize("T", [1, 16, 64])
+@pytest.mark.parametrize("T", [1, 16, 64, 200])
 def test_shared_experts_deepseek_shape(T, device):
     from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
     banner(f"deepseek shared T={T}")

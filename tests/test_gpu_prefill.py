@@ -1,0 +1,128 @@
+"""The tiled INT4 prefill kernel (128-row token groups x 128 weight rows) on
+the GPU vs the fp32 dequantise-then-matmul oracle.  Covers several token
+groups per expert, ragged last groups, one expert taking every row, f16 and
+bf16 activations, the sorted-row GEMM on both kernels (N % 128 == 0 tiles,
+N = 96 does not), group size 256 (the untiled kernel), and mixed tiers where
+BF16 / INT8 groups and INT4 groups run on different kernels in one layer.
+Tolerance: relative L2 <= 0.5%."""
+import numpy as np
+import pytest
+import torch
+
+from exq_amd import synth
+from oracle import moe, quant, routing
+from tests._helpers import assert_close_rel, banner, oracle_int4_layer
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-3
+
+WIDE = synth.MoeConfig("prefill_wide", 41, 1024, 512, 8, 2, True)
+
+
+def _pack(E, I, H, seed, device, group_size=128):
+    from exq_amd.kernels import pack_experts_int4
+    w13, w2 = synth.expert_weights_gpu(E, I, H, seed, device)
+    p13, s13 = pack_experts_int4(w13, group_size=group_size)
+    p2, s2 = pack_experts_int4(w2, group_size=group_size)
+    return p13, s13, p2, s2
+
+
+def _hidden(T, H, seed, device, dtype):
+    return torch.from_numpy(synth.hidden_np(T, H, seed)).to(dtype).to(device)
+
+
+@pytest.mark.parametrize("T,dtype", [(300, torch.bfloat16), (300, torch.float16),
+                                     (1000, torch.bfloat16)])
+def test_prefill_fused_zipf_routing(T, dtype, device):
+    from exq_amd.kernels import fused_experts
+    cfg = WIDE
+    banner(f"prefill fused T={T} {dtype}")
+    p13, s13, p2, s2 = _pack(cfg.n_experts, cfg.inter, cfg.hidden, 900, device)
+    ids, w = synth.routing(cfg, T)
+    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
+    assert counts.max() > 128  # several token groups for the busiest expert
+    x = _hidden(T, cfg.hidden, 901 + T, device, dtype)
+    so = torch.empty(T * cfg.top_k, dtype=torch.int64, device=device)
+    ends = torch.empty(cfg.n_experts + 1, dtype=torch.int32, device=device)
+    out = fused_experts(x, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                        torch.from_numpy(ids).to(device), sort_order_out=so,
+                        expert_ends_out=ends)
+    torch.cuda.synchronize()
+    r_so, r_ends, _ = routing.sort_tokens_by_expert(ids, cfg.n_experts)
+    assert np.array_equal(so.cpu().numpy(), r_so)
+    assert np.array_equal(ends.cpu().numpy(), r_ends)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, f"prefill fused T={T} {dtype}")
+
+
+def test_prefill_one_expert_takes_all_rows(device):
+    """Every row on one expert: 600 rows = four full 128-row groups + 88."""
+    from exq_amd.kernels import fused_experts
+    cfg = WIDE
+    banner("prefill one expert")
+    T = 300
+    p13, s13, p2, s2 = _pack(cfg.n_experts, cfg.inter, cfg.hidden, 910, device)
+    ids = np.full((T, 2), 5, dtype=np.int64)
+    ids[:, 1] = 5
+    rng = np.random.default_rng(11)
+    w = rng.random((T, 2)).astype(np.float32)
+    x = _hidden(T, cfg.hidden, 912, device, torch.bfloat16)
+    out = fused_experts(x, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                        torch.from_numpy(ids).to(device))
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, "prefill one expert")
+
+
+def test_prefill_group_size_256_untiled(device):
+    """group_size 256 is not tiled: the 64-row grouped kernel runs instead."""
+    from exq_amd.kernels import fused_experts
+    cfg = WIDE
+    banner("prefill group 256")
+    T = 200
+    p13, s13, p2, s2 = _pack(cfg.n_experts, cfg.inter, cfg.hidden, 920, device, group_size=256)
+    assert s13.shape[-1] == cfg.hidden // 256
+    ids, w = synth.routing(cfg, T)
+    x = _hidden(T, cfg.hidden, 921, device, torch.bfloat16)
+    out = fused_experts(x, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                        torch.from_numpy(ids).to(device))
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, "prefill group 256")
+
+
+@pytest.mark.parametrize("N", [256, 96])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_sorted_int4_gemm(N, dtype, device):
+    from exq_amd.kernels import moe_int4_forward, pack_experts_int4
+    banner(f"prefill sorted gemm N={N} {dtype}")
+    E, K, T, k = 8, 512, 300, 2
+    cfg = synth.MoeConfig("sorted", 43, K, N, E, k, True)
+    rng = np.random.default_rng(N)
+    w = torch.from_numpy((rng.standard_normal((E, N, K)) * 0.02).astype(np.float32)).to(device)
+    p, s = pack_experts_int4(w)
+    ids, _ = synth.routing(cfg, T)
+    x = _hidden(T, K, 930, device, dtype)
+    out = moe_int4_forward(x, p, s, torch.from_numpy(ids).to(device), E)
+    r_so, r_ends, _ = routing.sort_tokens_by_expert(ids, E)
+    a = moe.gather_hidden(x.float().cpu().numpy(), r_so, k)
+    ref = moe.grouped_gemm_sorted(a, quant.dequant_int4(p.cpu().numpy(), s.cpu().numpy()), r_ends)
+    assert_close_rel(out, ref, TOL, f"sorted gemm N={N} {dtype}")
+
+
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float16])
+def test_prefill_mixed_tiers(act, device):
+    """BF16 / INT8 token groups on the grouped kernel, INT4 on the tiled one."""
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    banner(f"prefill mixed tiers {act}")
+    T = 400
+    cfg = synth.MoeConfig("mix_prefill", 44, 512, 256, 16, 4, False)
+    w13, w2 = synth.expert_weights_gpu(16, 256, 512, 71, device)
+    tiers = synth.mixed_tiers(16, 71)
+    assert set(tiers) == {0, 1, 2}
+    bank = MixedExpertBank.from_weights(w13, w2, tiers, act_dtype=act)
+    ids, w = synth.routing(cfg, T)
+    x = _hidden(T, 512, 940, device, act)
+    out = fused_experts_mixed(x, bank, torch.from_numpy(w).to(device),
+                              torch.from_numpy(ids).to(device))
+    from tests.test_gpu_mixed import _oracle
+    assert_close_rel(out, _oracle(bank, x, ids, w), TOL, f"prefill mixed {act}")
