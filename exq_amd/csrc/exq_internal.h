@@ -7,8 +7,8 @@
 namespace exq {
 
 // Tokens of one expert are processed in groups of at most this many rows:
-// four 16-row MFMA tiles for BF16 / INT8 experts, eight for INT4 experts
-// (the tiled prefill kernel's 128-row tile).
+// four 16-row MFMA tiles on the grouped kernel, eight on the tiled prefill
+// kernels (128-row tiles).
 constexpr int kTokenGroup = 64;
 constexpr int kTokenGroupI4 = 128;
 
@@ -44,7 +44,7 @@ struct Bank {
 };
 
 struct GemmArgs {
-  const int* hdr;          // hdr[0] = number of token groups, hdr[1] = first INT4 group
+  const int* hdr;          // [0] token groups, [1] first INT4 group, [2] first INT8 group
   const TgEntry* tg;
   int n_blocks;            // row blocks per token group
   const uint16_t* x;       // activations (f16/bf16 bits)
@@ -60,20 +60,21 @@ struct GemmArgs {
   int64_t out_stride;
   int H;
   int skip_i4;             // INT4 token groups belong to the tiled kernel: skip them
+  int skip_bf;             // BF16 token groups belong to the tiled kernel: skip them
 };
 
-// Tiled prefill GEMM (prefill.hip) over the INT4 token groups of the plan,
-// entries [hdr[1], hdr[0]) of the token-group list (cnt <= kTokenGroupI4):
-// work-group tile = 128 expert-sorted rows x 128 weight rows.  It needs
-// the per-row group sums of its activations, scaled by the nibble base,
-// from launch_group_rowsum (rs [K / group_size][rs_rows]; GATEUP rows are
-// tokens, DOWN / PLAIN rows are expert-sorted positions).
-bool tile_gemm_applies(int mode, int n_rows, int inter, int K, int group_size);
-int64_t tile_rowsum_floats(int64_t rows, int64_t K);  // rs floats for any group size
+// Tiled prefill GEMMs (prefill.hip): work-group tile = 128 expert-sorted rows
+// x 128 weight rows over the token groups of one tier (cnt <= kTokenGroupI4):
+// INT4 groups are entries [hdr[1], hdr[0]) of the list, BF16 groups [0,
+// hdr[2]).  The INT4 kernel needs the per-row group sums of its activations,
+// scaled by the nibble base, from launch_group_rowsum (rs [K / 128][rs_rows];
+// GATEUP rows are tokens, DOWN / PLAIN rows are expert-sorted positions).
+bool tile_gemm_applies(int tier, int mode, int n_rows, int inter, int K, int group_size);
+int64_t tile_rowsum_floats(int64_t rows, int64_t K);
 int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows, int K, int gs,
                         float* out, hipStream_t s);
-int launch_tile_gemm(int mode, bool bf, const GemmArgs& a, const float* rs, int64_t rs_rows,
-                     int64_t x_bytes, int64_t tg_cap, hipStream_t s);
+int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
+                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s);
 
 // Parameters of the routing-plan kernel (one work-group).
 struct RoutePlanParams {
@@ -82,12 +83,13 @@ struct RoutePlanParams {
   int T, k, kp, E, Ep;  // kp = k + n_shared, Ep = E + n_shared
   int n;                // T * kp
   const int8_t* tier;   // [Ep] or null (all INT4)
-  int* hdr;             // hdr[0] = number of token groups, hdr[1] = first INT4 group
+  int* hdr;             // [0] token groups, [1] first INT4 group, [2] first INT8 group
   int* ends;            // [Ep + 1]
   int* sorted;          // [n] slot ids in expert-sorted order
   TgEntry* tg;          // [tg_cap]
   int tg_cap;
   int i4_group;         // rows per INT4 token group (kTokenGroup or kTokenGroupI4)
+  int bf_group;         // rows per BF16 token group (kTokenGroup or kTokenGroupI4)
   int* counters;        // combine arrival counters, zeroed here
   int n_counters;
   int64_t* sort_order_out;  // optional [T*k]

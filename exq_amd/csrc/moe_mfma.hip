@@ -360,8 +360,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a, const TgEntry& te, 
 template <bool BF, int MODE>
 __global__ void __launch_bounds__(NTH, 2) moe_gemm_kernel(GemmArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[WG_LDS];
-  // INT4 token groups (the tail of the list) go to the tiled kernel when it runs.
-  const int n_tg = a.skip_i4 ? a.hdr[1] : a.hdr[0];
+  // Token groups are ordered BF16, INT8, INT4; the BF16 head and the INT4 tail
+  // go to the tiled kernels when those run.
+  const int lo = a.skip_bf ? a.hdr[2] : 0;
+  const int n_tg = (a.skip_i4 ? a.hdr[1] : a.hdr[0]) - lo;
   const int U = n_tg * a.n_blocks;
   // XCD-aware order: work-group i runs on XCD i % 8, so each XCD takes a
   // contiguous range of units and neighbouring blocks of one token group
@@ -372,7 +374,7 @@ __global__ void __launch_bounds__(NTH, 2) moe_gemm_kernel(GemmArgs a) {
   if (local >= per || unit >= U) return;
   const int tgi = unit / a.n_blocks;
   const int blk = unit - tgi * a.n_blocks;
-  const TgEntry te = a.tg[tgi];
+  const TgEntry te = a.tg[lo + tgi];
   if (te.tier == 0) {
     gemm_body<0, BF, MODE>(a, te, blk, lds);
   } else if (te.tier == 1) {
@@ -540,14 +542,19 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   rp.sorted = reinterpret_cast<int*>(ws + L.sorted);
   rp.tg = reinterpret_cast<TgEntry*>(ws + L.tg);
   rp.tg_cap = (int)L.tg_cap;
-  // INT4 experts run on the tiled kernel (128-row token groups) when both
-  // projections fit it and the gathered activations are 32-bit addressable.
+  // INT4 and BF16 experts run on the tiled kernels (128-row token groups)
+  // when both projections fit them and the gathered activations are 32-bit
+  // addressable; INT8 experts (and everything else) on the grouped kernel.
   const int gs = (int)p->group_size;
-  const bool tile = tile_gemm_applies(MODE_GATEUP, 2 * I, I, H, gs) &&
-                    tile_gemm_applies(MODE_DOWN, H, I, I, gs) &&
-                    (int64_t)T * H * 2 <= 0x7fffffffLL &&
+  const bool x32 = (int64_t)T * H * 2 <= 0x7fffffffLL;
+  const bool tile = x32 && tile_gemm_applies(2, MODE_GATEUP, 2 * I, I, H, gs) &&
+                    tile_gemm_applies(2, MODE_DOWN, H, I, I, gs) &&
                     tile_rowsum_floats(L.n, I) * 4 <= 0x7fffffffLL;
+  const bool tile_bf = tier != nullptr && x32 &&
+                       tile_gemm_applies(0, MODE_GATEUP, 2 * I, I, H, gs) &&
+                       tile_gemm_applies(0, MODE_DOWN, H, I, I, gs);
   rp.i4_group = tile ? kTokenGroupI4 : kTokenGroup;
+  rp.bf_group = tile_bf ? kTokenGroupI4 : kTokenGroup;
   rp.counters = nullptr;
   rp.n_counters = 0;
   rp.sort_order_out = sort_order_out;
@@ -605,6 +612,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     g.group_size = gs;
     g.inter = I;
     g.skip_i4 = tile ? 1 : 0;
+    g.skip_bf = tile_bf ? 1 : 0;
     // Without a tier array every expert is INT4: the tiled kernel does it all.
     const bool old_kernel = !tile || tier != nullptr;
     float* rs = reinterpret_cast<float*>(ws + L.rs);
@@ -621,10 +629,14 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
+    if (tile_bf) {
+      st = launch_tile_gemm(0, MODE_GATEUP, bf, g, nullptr, 0, (int64_t)T * H * 2, L.tg_cap, s);
+      if (st) return st;
+    }
     if (tile) {
       st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
       if (st) return st;
-      st = launch_tile_gemm(MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s);
+      st = launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s);
       if (st) return st;
     }
     st = record_stage(2, s);
@@ -643,10 +655,14 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
+    if (tile_bf) {
+      st = launch_tile_gemm(0, MODE_DOWN, bf, g, nullptr, 0, 0, L.tg_cap, s);
+      if (st) return st;
+    }
     if (tile) {
       st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
       if (st) return st;
-      st = launch_tile_gemm(MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s);
+      st = launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s);
       if (st) return st;
     }
   }
@@ -696,7 +712,8 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
   int* hdr = reinterpret_cast<int*>(ws);
   TgEntry* tg = reinterpret_cast<TgEntry*>(ws + tg_off);
   const bool bf = act_dtype == EXQ_DTYPE_BF16;
-  const bool tile = tier == 2 && tile_gemm_applies(MODE_PLAIN, (int)N, 0, (int)K, (int)gs) &&
+  const bool tile = (tier == 2 || tier == 0) &&
+                    tile_gemm_applies(tier, MODE_PLAIN, (int)N, 0, (int)K, (int)gs) &&
                     tile_rowsum_floats(n_rows, K) * 4 <= 0x7fffffffLL;
   int st = launch_tg_from_ends(ends, (int)n_experts, mask, tier,
                                tile ? kTokenGroupI4 : kTokenGroup, hdr, tg, (int)tg_cap, s);
@@ -713,11 +730,12 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
   g.group_size = (int)gs;
   g.out = c;
   g.out_stride = N;
+  if (tile && tier == 0) return launch_tile_gemm(0, MODE_PLAIN, bf, g, nullptr, 0, 0, tg_cap, s);
   if (tile) {
     float* rs = reinterpret_cast<float*>(ws + rs_off);
     st = launch_group_rowsum(bf, g.x, K, n_rows, (int)K, (int)gs, rs, s);
     if (st) return st;
-    return launch_tile_gemm(MODE_PLAIN, bf, g, rs, n_rows, 0, tg_cap, s);
+    return launch_tile_gemm(2, MODE_PLAIN, bf, g, rs, n_rows, 0, tg_cap, s);
   }
   return launch_gemm<MODE_PLAIN>(bf, g, tg_cap * g.n_blocks, s);
 }

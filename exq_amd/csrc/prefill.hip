@@ -1,5 +1,6 @@
-// prefill.hip -- tiled grouped GEMM for INT4 experts on gfx950 MFMA (the
-// prefill / large-batch path of the fused layer and of exq_moe_int4_gemm).
+// prefill.hip -- tiled grouped GEMMs for INT4 and BF16 experts on gfx950 MFMA
+// (the prefill / large-batch path of the fused layers and of the sorted-row
+// GEMM entry points).
 //
 // Work decomposition.  One work-group computes a 128 x 128 output tile: the
 // <= 128 expert-sorted rows of one token group (one expert) times 128 weight
@@ -137,11 +138,101 @@ __device__ __forceinline__ uint32_t to_act_bits(float v) {
 __device__ __forceinline__ int b_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 struct TileArgs {
-  const float* rs;   // [K / group_size][rs_rows]: base * (row sum over the group)
+  const float* rs;   // INT4: [K / 128][rs_rows] base * (row sum over the group)
   int rs_rows;
   int64_t x_bytes;   // bytes addressable from a.x (GATEUP gather)
   int n_tiles;       // weight tiles per expert (I / 64 for GATEUP, rows / 128 otherwise)
 };
+
+// ---- shared pieces of the tiled kernels --------------------------------------
+
+// Unit (token group, weight tile) of this work-group over token groups
+// [t0, t0 + n), in XCD-aware order: work-group i runs on XCD i % 8 and each
+// XCD takes a contiguous range of units; inside it, 64 consecutive units are
+// 8 token groups x 8 weight tiles, so concurrently running tiles share
+// activation and weight chunks in that XCD's L2.  False: no unit.
+__device__ __forceinline__ bool tile_unit(const GemmArgs& a, int t0, int n, int NT, TgEntry& te,
+                                          int& nt) {
+  const int U = ((n + 7) >> 3) * 8 * NT;
+  const int per = (U + 7) >> 3;
+  const int local = blockIdx.x >> 3;
+  const int v = (blockIdx.x & 7) * per + local;
+  if (local >= per || v >= U) return false;
+  const int tb = v / (8 * NT);
+  const int rem = v - tb * 8 * NT;
+  nt = rem >> 3;
+  const int tgi = tb * 8 + (rem & 7);
+  if (tgi >= n) return false;
+  te = a.tg[t0 + tgi];
+  return true;
+}
+
+// Weight row (within the expert) of LDS weight row rho of tile nt.
+template <int MODE>
+__device__ __forceinline__ int tile_wrow(const GemmArgs& a, int nt, int rho) {
+  if constexpr (MODE == MODE_GATEUP)
+    return rho < 64 ? nt * 64 + rho : a.inter + nt * 64 + (rho - 64);
+  else
+    return nt * 128 + rho;
+}
+
+// First LDS weight row of n-tile t of wave column wn (NTW tiles per wave).
+// GATEUP: the first half of a wave's tiles are gate rows, the second half the
+// up rows of the same j.
+template <int MODE, int NTW>
+__device__ __forceinline__ int tile_brow(int wn, int t) {
+  constexpr int HALF = NTW / 2;
+  if constexpr (MODE == MODE_GATEUP)
+    return t < HALF ? wn * HALF * 16 + t * 16 : 64 + wn * HALF * 16 + (t - HALF) * 16;
+  else
+    return wn * NTW * 16 + t * 16;
+}
+
+// Activation row (GATEUP: token) of tile row m; rows past the group repeat
+// its last row (finite values whose outputs are never stored).
+template <int MODE>
+__device__ __forceinline__ int tile_xrow(const GemmArgs& a, const TgEntry& te, int m) {
+  const int mm = m < te.cnt ? m : te.cnt - 1;
+  if constexpr (MODE == MODE_GATEUP)
+    return a.row_slot[te.pos0 + mm] / a.slot_div;
+  else
+    return te.pos0 + mm;
+}
+
+// Store a wave's finished sub-tile (rows wm*MT*16.., MFMA output layout).
+template <bool BF, int MODE, int MT, int NTW>
+__device__ __forceinline__ void tile_store(const GemmArgs& a, const TgEntry& te, int nt, int wm,
+                                           int wn, int r16, int kq,
+                                           const f32x4_t (&tot)[MT][NTW]) {
+  constexpr int HALF = NTW / 2;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int v_ = 0; v_ < 4; ++v_) {
+      const int m = wm * MT * 16 + mt * 16 + kq * 4 + v_;
+      if (m >= te.cnt) continue;
+      const int pos = te.pos0 + m;
+      if constexpr (MODE == MODE_GATEUP) {
+        uint16_t* mid = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
+                        nt * 64 + wn * HALF * 16 + r16;
+#pragma unroll
+        for (int t = 0; t < HALF; ++t)
+          mid[t * 16] = (uint16_t)to_act_bits<BF>(silu_f32(tot[mt][t][v_]) * tot[mt][t + HALF][v_]);
+      } else if constexpr (MODE == MODE_PLAIN) {
+        uint16_t* c = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
+                      nt * 128 + wn * NTW * 16 + r16;
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) c[t * 16] = (uint16_t)to_act_bits<BF>(tot[mt][t][v_]);
+      } else {
+        const int slot = a.row_slot[pos];
+        float* part = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.out_stride + nt * 128 +
+                      wn * NTW * 16 + r16;
+#pragma unroll
+        for (int t = 0; t < NTW; ++t) part[t * 16] = tot[mt][t][v_];
+      }
+    }
+  }
+}
 
 // MT = m-tiles (16 rows) per wave: 4 -> waves 2 x 2 of 64 x 64; 8 -> 1 x 4 of 128 x 32.
 template <bool BF, int MODE, int MT>
@@ -149,32 +240,15 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   constexpr int WAVES_M = 8 / MT;
   constexpr int WAVES_N = 4 / WAVES_M;
   constexpr int NTW = 8 / WAVES_N;  // n-tiles (16 weight rows) per wave
-  constexpr int HALF = NTW / 2;
   constexpr int RSR = MT / 4;       // row sums held per lane (64 rows each)
   __shared__ __attribute__((aligned(1024))) unsigned char sA0[A_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sA1[A_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sB0[B_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sB1[B_STAGE];
 
-  // ---- unit: (token group, weight tile), XCD-aware order -------------------
-  // Work-group i runs on XCD i % 8 and each XCD takes a contiguous range of
-  // units; inside it, 64 consecutive units are 8 token groups x 8 weight
-  // tiles, so concurrently running tiles share activation and weight chunks
-  // in that XCD's L2.
-  const int t0 = a.hdr[1];
-  const int n4 = a.hdr[0] - t0;
-  const int NT = ta.n_tiles;
-  const int U = ((n4 + 7) >> 3) * 8 * NT;
-  const int per = (U + 7) >> 3;
-  const int local = blockIdx.x >> 3;
-  const int v = (blockIdx.x & 7) * per + local;
-  if (local >= per || v >= U) return;
-  const int tb = v / (8 * NT);
-  const int rem = v - tb * 8 * NT;
-  const int nt = rem >> 3;
-  const int tgi = tb * 8 + (rem & 7);
-  if (tgi >= n4) return;
-  const TgEntry te = a.tg[t0 + tgi];
+  TgEntry te;
+  int nt;
+  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, te, nt)) return;  // INT4 groups
   const int cnt = te.cnt, pos0 = te.pos0;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -188,27 +262,9 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   const int widx = a.w.index ? a.w.index[te.e] : te.e;
   const int64_t ebase = (int64_t)widx * a.n_rows;
   const int rowbytes = K / 2;
-  auto wrow = [&](int rho) -> int {  // weight row (within the expert) of LDS row rho
-    if constexpr (MODE == MODE_GATEUP)
-      return rho < 64 ? nt * 64 + rho : a.inter + nt * 64 + (rho - 64);
-    else
-      return nt * 128 + rho;
-  };
-  auto brow = [&](int t) -> int {  // first LDS weight row of this wave's n-tile t
-    if constexpr (MODE == MODE_GATEUP)
-      return t < HALF ? wn * HALF * 16 + t * 16 : 64 + wn * HALF * 16 + (t - HALF) * 16;
-    else
-      return wn * NTW * 16 + t * 16;
-  };
-  // Row m (0..127) of the tile: rows past the group repeat its last row
-  // (finite values whose outputs are never stored).
-  auto x_row = [&](int m) -> int {  // activation row (GATEUP: token) of tile row m
-    const int mm = m < cnt ? m : cnt - 1;
-    if constexpr (MODE == MODE_GATEUP)
-      return a.row_slot[pos0 + mm] / a.slot_div;
-    else
-      return pos0 + mm;
-  };
+  auto wrow = [&](int rho) { return tile_wrow<MODE>(a, nt, rho); };
+  auto brow = [&](int t) { return tile_brow<MODE, NTW>(wn, t); };
+  auto x_row = [&](int m) { return tile_xrow<MODE>(a, te, m); };
 
   const __amdgpu_buffer_rsrc_t wr =
       make_rsrc(a.w.i4 + ebase * rowbytes, (int64_t)a.n_rows * rowbytes);
@@ -344,34 +400,118 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
 #undef EXQ_TILE_CHUNK
   wait_vm_all();  // the last (empty) prefetch has drained before the work-group ends
 
-  // ---- epilogue --------------------------------------------------------------
+  tile_store<BF, MODE, MT, NTW>(a, te, nt, wm, wn, r16, kq, tot);
+}
+
+// ---- BF16 experts ------------------------------------------------------------
+// Same tile and unit order over the BF16 token groups [0, hdr[2]); chunks of
+// 64 k: activations and weights both 128 rows x 128 B per stage, swizzled in
+// 16-byte columns with c ^ f(r), f(r) = (r ^ (r >> 3)) & 7 (conflict-free
+// ds_read_b128 of 16 consecutive rows at one column for 8 or 16 lanes per
+// cycle).  Lane (r, q) at k-step s holds k = 16q + 8s .. +7 of both operands;
+// the fp32 accumulators run over the whole contraction.
+constexpr int KCB = 64;
+constexpr int AB_STAGE = 128 * KCB * 2;  // 16 KiB per operand and stage
+
+__device__ __forceinline__ int bf_swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+template <bool BF, int MODE>
+__global__ void __launch_bounds__(TT, 2) tile_gemm_bf16_kernel(GemmArgs a, TileArgs ta) {
+  constexpr int MT = 4, NTW = 4, WAVES_N = 2;
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[AB_STAGE];
+
+  TgEntry te;
+  int nt;
+  if (!tile_unit(a, 0, a.hdr[2], ta.n_tiles, te, nt)) return;  // BF16 groups
+  const int cnt = te.cnt, pos0 = te.pos0;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int K = a.K;
+  const int nch = K / KCB;
+  const int widx = a.w.index ? a.w.index[te.e] : te.e;
+  const int64_t ebase = (int64_t)widx * a.n_rows;
+  const int rowbytes = K * 2;
+
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(a.w.bf16 + ebase * K, (int64_t)a.n_rows * rowbytes);
+  const __amdgpu_buffer_rsrc_t xr =
+      MODE == MODE_GATEUP
+          ? make_rsrc(a.x, ta.x_bytes)
+          : make_rsrc(a.x + (int64_t)pos0 * a.x_stride, (int64_t)cnt * a.x_stride * 2);
+  const __amdgpu_buffer_rsrc_t wnull = make_rsrc(a.w.bf16, 0);
+  const __amdgpu_buffer_rsrc_t xnull = make_rsrc(a.x, 0);
+
+  // DMA: instruction q of this wave fills LDS rows 8j..8j+7 (j = 4 wave + q),
+  // 8 columns each.
+  int voffA[4], voffB[4];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-    for (int v_ = 0; v_ < 4; ++v_) {
-      const int m = wm * MT * 16 + mt * 16 + kq * 4 + v_;
-      if (m >= cnt) continue;
-      const int pos = pos0 + m;
-      if constexpr (MODE == MODE_GATEUP) {
-        uint16_t* mid = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
-                        nt * 64 + wn * HALF * 16 + r16;
-#pragma unroll
-        for (int t = 0; t < HALF; ++t)
-          mid[t * 16] = (uint16_t)to_act_bits<BF>(silu_f32(tot[mt][t][v_]) * tot[mt][t + HALF][v_]);
-      } else if constexpr (MODE == MODE_PLAIN) {
-        uint16_t* c = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
-                      nt * 128 + wn * NTW * 16 + r16;
-#pragma unroll
-        for (int t = 0; t < NTW; ++t) c[t * 16] = (uint16_t)to_act_bits<BF>(tot[mt][t][v_]);
-      } else {
-        const int slot = a.row_slot[pos];
-        float* part = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.out_stride + nt * 128 +
-                      wn * NTW * 16 + r16;
-#pragma unroll
-        for (int t = 0; t < NTW; ++t) part[t * 16] = tot[mt][t][v_];
-      }
-    }
+  for (int q = 0; q < 4; ++q) {
+    const int r = (wave * 4 + q) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ bf_swz(r & 15);
+    const int xrow = tile_xrow<MODE>(a, te, r);
+    voffA[q] = (MODE == MODE_GATEUP ? xrow : xrow - pos0) * (int)a.x_stride * 2 + c * 16;
+    voffB[q] = tile_wrow<MODE>(a, nt, r) * rowbytes + c * 16;
   }
+  // Fragment of k-step s: column (2 kq + s) ^ f(r16) of the row.
+  const int colx = ((kq * 2) ^ bf_swz(r16)) * 16;
+  const int aoff = (wm * MT * 16 + r16) * 128 + colx;
+  const int boff = (tile_brow<MODE, NTW>(wn, 0) + r16) * 128 + colx;
+
+  auto prefetch = [&](int st, int ch) {
+    const bool ok = ch < nch;
+    const int chl = ok ? ch : 0;
+    unsigned char* A = st ? sA1 : sA0;
+    unsigned char* B = st ? sB1 : sB0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma16(ok ? xr : xnull, A + (wave * 4 + q) * 1024, voffA[q], chl * 128);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma16(ok ? wr : wnull, B + (wave * 4 + q) * 1024, voffB[q], chl * 128);
+  };
+
+  f32x4_t acc[MT][NTW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) acc[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#define EXQ_BF_CHUNK(ST)                                                                      \
+  do {                                                                                        \
+    const unsigned char* A_ = ST ? sA1 : sA0;                                                 \
+    const unsigned char* B_ = ST ? sB1 : sB0;                                                 \
+    _Pragma("unroll") for (int s = 0; s < 2; ++s) {                                           \
+      uint4 af[MT], bf[NTW];                                                                  \
+      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                       \
+          af[mt] = *reinterpret_cast<const uint4*>(A_ + (aoff ^ (s * 16)) + mt * 16 * 128);   \
+      _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                         \
+          bf[t] = *reinterpret_cast<const uint4*>(                                            \
+              B_ + (boff ^ (s * 16)) +                                                        \
+              (tile_brow<MODE, NTW>(wn, t) - tile_brow<MODE, NTW>(wn, 0)) * 128);             \
+      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                       \
+          _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                     \
+              acc[mt][t] = mfma16<BF>(af[mt], bf[t], acc[mt][t]);                             \
+    }                                                                                         \
+  } while (0)
+
+  prefetch(0, 0);
+  for (int ch = 0; ch < nch; ch += 2) {
+    chunk_barrier();
+    prefetch(1, ch + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    EXQ_BF_CHUNK(0);
+    if (ch + 1 >= nch) break;
+    chunk_barrier();
+    prefetch(0, ch + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    EXQ_BF_CHUNK(1);
+  }
+#undef EXQ_BF_CHUNK
+  wait_vm_all();
+  tile_store<BF, MODE, MT, NTW>(a, te, nt, wm, wn, r16, kq, acc);
 }
 
 // out[g][r] = base * sum_{k in group g} x[r, k] (fp32 sums of the 16-bit
@@ -416,16 +556,17 @@ __global__ void __launch_bounds__(256) group_rowsum_kernel(const uint16_t* __res
 
 }  // namespace
 
-bool tile_gemm_applies(int mode, int n_rows, int inter, int K, int group_size) {
+bool tile_gemm_applies(int tier, int mode, int n_rows, int inter, int K, int group_size) {
   if (K < KC || K % KC != 0 || K > 65536) return false;
-  if (group_size != KC) return false;  // one chunk = one scale group
+  if (tier == 2 && group_size != KC) return false;  // one chunk = one scale group
+  if (tier == 1) return false;
   if (mode == MODE_GATEUP) {
     if (inter % 64 != 0 || n_rows != 2 * inter) return false;
   } else if (n_rows % 128 != 0) {
     return false;
   }
-  // 32-bit buffer offsets within one expert's weights and scales
-  if ((int64_t)n_rows * (K / 2) > 0x7fffffffLL) return false;
+  // 32-bit buffer offsets within one expert's weights
+  if ((int64_t)n_rows * (tier == 2 ? K / 2 : K * 2) > 0x7fffffffLL) return false;
   return true;
 }
 
@@ -445,19 +586,25 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
 }
 
 template <int MODE>
-static int launch_tile_mode(bool bf, const GemmArgs& a, const TileArgs& t, int64_t grid,
-                            hipStream_t s) {
+static int launch_tile_mode(int tier, bool bf, const GemmArgs& a, const TileArgs& t,
+                            int64_t grid, hipStream_t s) {
+  const dim3 g((unsigned)grid), b(TT);
+  if (tier == 0) {
+    if (bf)
+      hipLaunchKernelGGL((tile_gemm_bf16_kernel<true, MODE>), g, b, 0, s, a, t);
+    else
+      hipLaunchKernelGGL((tile_gemm_bf16_kernel<false, MODE>), g, b, 0, s, a, t);
+    return check_launch("tile_gemm_bf16_kernel");
+  }
   if (bf)
-    hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 4>), dim3((unsigned)grid), dim3(TT), 0, s, a,
-                       t);
+    hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 4>), g, b, 0, s, a, t);
   else
-    hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 4>), dim3((unsigned)grid), dim3(TT), 0, s,
-                       a, t);
+    hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 4>), g, b, 0, s, a, t);
   return check_launch("tile_gemm_kernel");
 }
 
-int launch_tile_gemm(int mode, bool bf, const GemmArgs& a, const float* rs, int64_t rs_rows,
-                     int64_t x_bytes, int64_t tg_cap, hipStream_t s) {
+int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
+                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s) {
   TileArgs t;
   t.rs = rs;
   t.rs_rows = (int)rs_rows;
@@ -467,9 +614,9 @@ int launch_tile_gemm(int mode, bool bf, const GemmArgs& a, const float* rs, int6
   if (grid <= 0) return EXQ_SUCCESS;
   if (grid > INT32_MAX || rs_rows > INT32_MAX)
     return set_error(EXQ_ERROR_UNSUPPORTED, "tile_gemm: problem too large");
-  if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(bf, a, t, grid, s);
-  if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(bf, a, t, grid, s);
-  return launch_tile_mode<MODE_PLAIN>(bf, a, t, grid, s);
+  if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(tier, bf, a, t, grid, s);
+  if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(tier, bf, a, t, grid, s);
+  return launch_tile_mode<MODE_PLAIN>(tier, bf, a, t, grid, s);
 }
 
 }  // namespace exq

@@ -234,10 +234,11 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
   // Token groups, heaviest tier first so long work items start early.
   const int c = b < nb ? s.cnt[b] : 0;
   const int my_tier = (b < nb) ? (p.tier ? (int)p.tier[b] : 2) : -1;
-  const int gsz = my_tier == 2 ? p.i4_group : kTokenGroup;
+  const int gsz = my_tier == 2 ? p.i4_group : my_tier == 0 ? p.bf_group : kTokenGroup;
   const int ng = (c + gsz - 1) / gsz;
-  int base = 0, first_i4 = 0;
+  int base = 0, first_i4 = 0, first_i8 = 0;
   for (int tr = (p.tier ? 0 : 2); tr <= 2; ++tr) {
+    if (tr == 1) first_i8 = base;
     if (tr == 2) first_i4 = base;
     int tot;
     int off = block_excl_scan(my_tier == tr ? ng : 0, s.wsum, &tot);
@@ -259,6 +260,7 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
   if (threadIdx.x == 0) {
     p.hdr[0] = base < p.tg_cap ? base : p.tg_cap;
     p.hdr[1] = first_i4 < p.tg_cap ? first_i4 : p.tg_cap;
+    p.hdr[2] = first_i8 < p.tg_cap ? first_i8 : p.tg_cap;
   }
   for (int i = threadIdx.x; i < p.n_counters; i += RT) p.counters[i] = 0;
   if (base == 0 && p.out) {
@@ -301,6 +303,7 @@ __global__ void __launch_bounds__(RT) tg_from_ends_kernel(const int32_t* ends, i
   if (threadIdx.x == 0) {
     hdr[0] = base < tg_cap ? base : tg_cap;
     hdr[1] = tier == 2 ? 0 : hdr[0];
+    hdr[2] = tier == 0 ? hdr[0] : 0;
   }
 }
 

@@ -126,3 +126,27 @@ def test_prefill_mixed_tiers(act, device):
                               torch.from_numpy(ids).to(device))
     from tests.test_gpu_mixed import _oracle
     assert_close_rel(out, _oracle(bank, x, ids, w), TOL, f"prefill mixed {act}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_sorted_bf16_gemm_tiled(dtype, device):
+    """Unquantised sorted-row GEMM with N % 128 == 0 runs on the BF16 tiled
+    kernel; a masked expert's rows stay zero."""
+    from exq_amd.kernels import moe_grouped_gemm
+    banner(f"prefill grouped gemm tiled {dtype}")
+    rng = np.random.default_rng(5)
+    E, N, K, T, k = 8, 256, 384, 300, 2
+    W = torch.from_numpy((rng.standard_normal((E, N, K)) * 0.05).astype(np.float32)).to(dtype)
+    cfg = synth.MoeConfig("sorted_bf", 45, K, N, E, k, True)
+    ids, _ = synth.routing(cfg, T)
+    x = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(dtype)
+    mask = torch.ones(E, dtype=torch.int32)
+    mask[3] = 0
+    out = moe_grouped_gemm(x.to(device), W.to(device), torch.from_numpy(ids).to(device), E,
+                           expert_mask=mask.to(device))
+    r_so, r_ends, _ = routing.sort_tokens_by_expert(ids, E)
+    a = moe.gather_hidden(x.float().numpy(), r_so, k)
+    Wm = W.float().numpy().copy()
+    Wm[3] = 0
+    ref = moe.grouped_gemm_sorted(a, Wm, r_ends)
+    assert_close_rel(out, ref, TOL, f"grouped gemm tiled {dtype}")
