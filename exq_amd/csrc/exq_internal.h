@@ -96,8 +96,13 @@ struct RoutePlanParams {
   int32_t* ends_out;        // optional [E+1]
   void* out;                // zero-filled when no row is routed
   int64_t out_bytes;
+  int* blk_cnt;             // [route_plan_blocks(n) * Ep] scratch, or null (one block)
 };
 
+// Batches above this many slots are planned by several work-groups, which
+// need route_plan_blocks(n) * Ep ints of scratch (blk_cnt).
+constexpr int kRoutePlanOneBlock = 2048;
+int64_t route_plan_blocks(int64_t n);
 int launch_route_plan(const RoutePlanParams& p, hipStream_t stream);
 
 // Token groups from user-provided expert boundaries (sorted-row GEMM API).

@@ -453,7 +453,7 @@ namespace {
 
 // ---- workspace layout of the fused forward --------------------------------------
 struct FusedLayout {
-  size_t sync, hdr, ends, sorted, tg, mid, partial, rs, total;
+  size_t sync, hdr, ends, sorted, tg, mid, partial, rs, blk, total;
   int64_t n, tg_cap;
 };
 
@@ -478,6 +478,7 @@ FusedLayout fused_layout(const exq_moe_problem& p) {
   const int64_t rs_x = tile_rowsum_floats(p.n_tokens, p.hidden_size);
   const int64_t rs_mid = tile_rowsum_floats(L.n, p.inter_size);
   L.rs = off;       off = align_up(off + (size_t)(rs_x > rs_mid ? rs_x : rs_mid) * 4, 256);
+  L.blk = off;      off = align_up(off + (size_t)route_plan_blocks(L.n) * Ep * 4, 256);
   L.total = off;
   return L;
 }
@@ -561,6 +562,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   rp.ends_out = expert_ends_out;
   rp.out = out;
   rp.out_bytes = (int64_t)T * H * 2;
+  rp.blk_cnt = reinterpret_cast<int*>(ws + L.blk);
   struct HookReset {  // the hook is consumed by this call, whatever happens
     ~HookReset() { g_stage_events_set = false; }
   } hook_reset;

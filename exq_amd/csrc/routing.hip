@@ -200,38 +200,29 @@ __global__ void __launch_bounds__(RT) align_kernel(const void* ids, int ids_dtyp
 }
 
 // ---- fused-path routing plan -----------------------------------------------
-__global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
-  __shared__ RouteLds s;
-  auto key = [&](int slot) -> int {
-    const int t = slot / p.kp;
-    const int j = slot - t * p.kp;
-    if (j < p.k) {
-      int64_t v = load_index(p.ids, p.ids_dtype, (int64_t)t * p.k + j);
-      return (v >= 0 && v < p.E) ? (int)v : -1;
-    }
-    return p.E + (j - p.k);
-  };
-  const int nb = p.Ep;
-  histogram(p.n, nb, key, s.cnt);
-  const int b = threadIdx.x;
-  int t;
-  int ex = block_excl_scan(b < nb ? s.cnt[b] : 0, s.wsum, &t);
-  if (b < nb) {
-    s.start[b] = ex;
-    s.run[b] = ex;
+// Bucket of slot t*kp + j: routed id (dropped: -1) for j < k, shared expert
+// E + (j - k) otherwise.
+__device__ __forceinline__ int plan_key(const RoutePlanParams& p, int slot) {
+  const int t = slot / p.kp;
+  const int j = slot - t * p.kp;
+  if (j < p.k) {
+    int64_t v = load_index(p.ids, p.ids_dtype, (int64_t)t * p.k + j);
+    return (v >= 0 && v < p.E) ? (int)v : -1;
   }
-  if (threadIdx.x == 0) s.start[nb] = t;
-  __syncthreads();
+  return p.E + (j - p.k);
+}
+
+// Everything after the sort that needs only the bucket counts s.cnt and
+// starts s.start (one work-group): boundaries, token groups (tier order BF16,
+// INT8, INT4, so long work items start early), header, combine counters, and
+// the zero output of a layer with no routed row.
+__device__ void plan_tail(const RoutePlanParams& p, RouteLds& s) {
+  const int nb = p.Ep;
+  const int b = threadIdx.x;
   for (int e = threadIdx.x; e <= nb; e += RT) p.ends[e] = s.start[e];
   if (p.ends_out) {
     for (int e = threadIdx.x; e <= p.E; e += RT) p.ends_out[e] = s.start[e];
   }
-  stable_scatter(p.n, nb, key, s.run, s.masks, [&](int i, int, int pos) {
-    p.sorted[pos] = i;
-    if (p.sort_order_out) p.sort_order_out[pos] = i;
-  });
-
-  // Token groups, heaviest tier first so long work items start early.
   const int c = b < nb ? s.cnt[b] : 0;
   const int my_tier = (b < nb) ? (p.tier ? (int)p.tier[b] : 2) : -1;
   const int gsz = my_tier == 2 ? p.i4_group : my_tier == 0 ? p.bf_group : kTokenGroup;
@@ -267,6 +258,81 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
     uint32_t* o = reinterpret_cast<uint32_t*>(p.out);
     for (int64_t i = threadIdx.x; i < p.out_bytes / 4; i += RT) o[i] = 0u;
   }
+}
+
+// One work-group: histogram, scan, stable scatter, tail.
+__global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
+  __shared__ RouteLds s;
+  auto key = [&](int slot) { return plan_key(p, slot); };
+  const int nb = p.Ep;
+  histogram(p.n, nb, key, s.cnt);
+  const int b = threadIdx.x;
+  int t;
+  int ex = block_excl_scan(b < nb ? s.cnt[b] : 0, s.wsum, &t);
+  if (b < nb) {
+    s.start[b] = ex;
+    s.run[b] = ex;
+  }
+  if (threadIdx.x == 0) s.start[nb] = t;
+  __syncthreads();
+  stable_scatter(p.n, nb, key, s.run, s.masks, [&](int i, int, int pos) {
+    p.sorted[pos] = i;
+    if (p.sort_order_out) p.sort_order_out[pos] = i;
+  });
+  plan_tail(p, s);
+}
+
+// Large batches: the same plan over RB-slot blocks in three launches --
+// per-block bucket counts, one work-group that turns them into per-block
+// bucket offsets (block order keeps every bucket in ascending slot order)
+// and runs the tail, and a per-block stable scatter from those offsets.
+constexpr int RB = 1024;  // slots per block
+
+__global__ void __launch_bounds__(RT) route_count_kernel(RoutePlanParams p) {
+  __shared__ int cnt[MAX_BUCKETS];
+  const int lo = blockIdx.x * RB;
+  const int m = min(RB, p.n - lo);
+  const int nb = p.Ep;
+  histogram(m, nb, [&](int i) { return plan_key(p, lo + i); }, cnt);
+  for (int e = threadIdx.x; e < nb; e += RT) p.blk_cnt[(int64_t)blockIdx.x * nb + e] = cnt[e];
+}
+
+__global__ void __launch_bounds__(RT) route_scan_kernel(RoutePlanParams p, int nblk) {
+  __shared__ RouteLds s;
+  const int nb = p.Ep;
+  const int b = threadIdx.x;
+  int tot_b = 0;
+  if (b < nb)
+    for (int k = 0; k < nblk; ++k) tot_b += p.blk_cnt[(int64_t)k * nb + b];
+  if (b < nb) s.cnt[b] = tot_b;
+  int t;
+  const int ex = block_excl_scan(b < nb ? tot_b : 0, s.wsum, &t);
+  if (b < nb) {
+    s.start[b] = ex;
+    int run = ex;
+    for (int k = 0; k < nblk; ++k) {  // counts -> offsets, in place
+      const int c = p.blk_cnt[(int64_t)k * nb + b];
+      p.blk_cnt[(int64_t)k * nb + b] = run;
+      run += c;
+    }
+  }
+  if (threadIdx.x == 0) s.start[nb] = t;
+  __syncthreads();
+  plan_tail(p, s);
+}
+
+__global__ void __launch_bounds__(RT) route_scatter_kernel(RoutePlanParams p) {
+  __shared__ RouteLds s;
+  const int lo = blockIdx.x * RB;
+  const int m = min(RB, p.n - lo);
+  const int nb = p.Ep;
+  for (int e = threadIdx.x; e < nb; e += RT) s.run[e] = p.blk_cnt[(int64_t)blockIdx.x * nb + e];
+  __syncthreads();
+  stable_scatter(m, nb, [&](int i) { return plan_key(p, lo + i); }, s.run, s.masks,
+                 [&](int i, int, int pos) {
+                   p.sorted[pos] = lo + i;
+                   if (p.sort_order_out) p.sort_order_out[pos] = lo + i;
+                 });
 }
 
 // ---- token groups from user boundaries ------------------------------------------
@@ -309,9 +375,22 @@ __global__ void __launch_bounds__(RT) tg_from_ends_kernel(const int32_t* ends, i
 
 }  // namespace
 
+int64_t route_plan_blocks(int64_t n) { return n > kRoutePlanOneBlock ? cdiv(n, RB) : 0; }
+
 int launch_route_plan(const RoutePlanParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(RT), 0, stream, p);
-  return check_launch("route_plan_kernel");
+  const int64_t nblk = route_plan_blocks(p.n);
+  if (nblk == 0 || p.blk_cnt == nullptr) {
+    hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(RT), 0, stream, p);
+    return check_launch("route_plan_kernel");
+  }
+  hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)nblk), dim3(RT), 0, stream, p);
+  int st = check_launch("route_count_kernel");
+  if (st) return st;
+  hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(RT), 0, stream, p, (int)nblk);
+  st = check_launch("route_scan_kernel");
+  if (st) return st;
+  hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)nblk), dim3(RT), 0, stream, p);
+  return check_launch("route_scatter_kernel");
 }
 
 int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, int tier,
