@@ -19,7 +19,7 @@
 // global memory into LDS by buffer_load ... lds (16 B per lane, 64 lanes per
 // 1 KiB instruction), double-buffered: chunk c+1 is in flight while chunk c
 // is multiplied.  Both LDS images are XOR-swizzled in 16-byte columns so the
-// MFMA operand reads (16 rows, one column) hit distinct banks.
+// MFMA operand reads (16 rows, one column) are free of bank conflicts.
 //
 // Arithmetic.  Lane (r, q) of an MFMA 16x16x32 operand holds 8 k values; the
 // k assignment is chosen so that a lane's B values for the whole chunk are 16
@@ -132,10 +132,21 @@ __device__ __forceinline__ uint32_t to_act_bits(float v) {
   return BF ? f32_to_bf16_bits(v) : f32_to_f16_bits(v);
 }
 
-// Swizzle of the 16-byte column c of LDS weight row r (4 columns per 64-byte
-// row): conflict-free ds_read_b128 for 16 consecutive rows at one column
-// whether the LDS serves 8 or 16 lanes per cycle.
-__device__ __forceinline__ int b_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// LDS swizzles.  gfx950 serves a ds_read_b128 in four cycles of 256 bytes
+// (16-byte units u = (address >> 4) & 15); the lanes served together are those
+// with equal bit 5 and equal parity of bits 2..4 of the lane id (measured with
+// SQ_LDS_BANK_CONFLICT over a set of access patterns).  An MFMA operand read
+// (lane = row r + 16 q, column from q) is conflict-free when each such group
+// of 16 lanes covers 16 distinct units; these maps of the row's low 4 bits
+// achieve that:
+//   activation rows (256 B, 16 columns): c ^ a_swz(r)
+//   packed weight rows (64 B, 4 columns): c ^ b_swz(r)
+__device__ __forceinline__ int a_swz(int r) {
+  return (r & 3) | ((r >> 1) & 4) | (((r << 1) ^ r) & 8);
+}
+__device__ __forceinline__ int b_swz(int r) {
+  return ((r >> 3) & 1) | ((((r >> 2) ^ (r >> 3)) & 1) << 1);
+}
 
 struct TileArgs {
   const float* rs;   // INT4: [K / 128][rs_rows] base * (row sum over the group)
@@ -285,7 +296,7 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
 #pragma unroll
   for (int q = 0; q < 8; ++q) {  // LDS rows 4j..4j+3 per instruction, 16 columns each
     const int m = (wave * 8 + q) * 4 + (lane >> 4);
-    const int c = (lane & 15) ^ (m & 15);
+    const int c = (lane & 15) ^ a_swz(m & 15);
     const int xrow = x_row(m);
     voffA[q] = (MODE == MODE_GATEUP ? xrow : xrow - pos0) * (int)a.x_stride * 2 + c * 16;
   }
@@ -311,7 +322,7 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
 
   // LDS read offsets: A fragment of k-step s = aoff ^ (16 s) (+ 4 KiB per
   // m-tile); weight tile t = boff + bdel(t).
-  const int aoff = (wm * MT * 16 + r16) * 256 + (((kq * 4) ^ r16) * 16);
+  const int aoff = (wm * MT * 16 + r16) * 256 + (((kq * 4) ^ a_swz(r16)) * 16);
   const int boff = (brow(0) + r16) * 64 + ((kq ^ b_swz(r16)) * 16);
   uint32_t sc_raw[2][NTW];
   float rs_raw[2][RSR];
@@ -406,9 +417,8 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
 // ---- BF16 experts ------------------------------------------------------------
 // Same tile and unit order over the BF16 token groups [0, hdr[2]); chunks of
 // 64 k: activations and weights both 128 rows x 128 B per stage, swizzled in
-// 16-byte columns with c ^ f(r), f(r) = (r ^ (r >> 3)) & 7 (conflict-free
-// ds_read_b128 of 16 consecutive rows at one column for 8 or 16 lanes per
-// cycle).  Lane (r, q) at k-step s holds k = 16q + 8s .. +7 of both operands;
+// 16-byte columns with c ^ f(r), f(r) = (r ^ (r >> 3)) & 7 (measured free of
+// bank conflicts for the operand reads).  Lane (r, q) at k-step s holds k = 16q + 8s .. +7 of both operands;
 // the fp32 accumulators run over the whole contraction.
 constexpr int KCB = 64;
 constexpr int AB_STAGE = 128 * KCB * 2;  // 16 KiB per operand and stage
