@@ -607,9 +607,9 @@ static int launch_tile_mode(int tier, bool bf, const GemmArgs& a, const TileArgs
     return check_launch("tile_gemm_bf16_kernel");
   }
   if (bf)
-    hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 4>), g, b, 0, s, a, t);
+    hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 8>), g, b, 0, s, a, t);
   else
-    hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 4>), g, b, 0, s, a, t);
+    hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 8>), g, b, 0, s, a, t);
   return check_launch("tile_gemm_kernel");
 }
 
