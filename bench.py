@@ -60,6 +60,10 @@ def parse_args():
                     help="calibration copy + one eager pass, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summary", type=str, default="",
                     help="per-kernel mean of a rocprofv3 counter CSV")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the prefill configurations (DeepSeek-V2-Lite 2048, Mixtral 4096)")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --prefill-only: one eager call per configuration (counter runs)")
     return ap.parse_args()
 
 
@@ -242,6 +246,63 @@ def _graph_time(fn, reps, warmup=3):
     return e0.elapsed_time(e1) / reps
 
 
+def _deepseek_bank(cfg, layer, dev):
+    """DeepSeek-V2-Lite layer: 64 INT4 routed experts + 2 BF16 shared experts."""
+    from exq_amd import synth
+    from exq_amd.kernels import MixedExpertBank
+    w13, w2 = synth.expert_weights_gpu(cfg.n_experts, cfg.inter, cfg.hidden,
+                                       synth.seed_for(cfg, layer), dev)
+    s13, s2 = synth.expert_weights_gpu(cfg.n_shared, cfg.inter, cfg.hidden,
+                                       synth.seed_for(cfg, layer) + 500, dev)
+    return MixedExpertBank.from_weights(w13, w2, [2] * cfg.n_experts, shared_w13=s13,
+                                        shared_w2=s2, shared_tier=0)
+
+
+def _int4_layer(cfg, layer, dev):
+    from exq_amd import synth
+    from exq_amd.kernels import pack_experts_int4
+    w13, w2 = synth.expert_weights_gpu(cfg.n_experts, cfg.inter, cfg.hidden,
+                                       synth.seed_for(cfg, layer), dev)
+    return pack_experts_int4(w13) + pack_experts_int4(w2)
+
+
+def _prefill_call(dev, name, weights=None):
+    """(name, T, fn, flops) of one prefill configuration: DeepSeek-V2-Lite (2048
+    tokens, top-6 + 2 shared, `weights` a MixedExpertBank) or Mixtral (4096
+    tokens, top-2, `weights` the packed (w13, s13, w2, s2)); built if None."""
+    import numpy as np
+    import torch
+    from exq_amd import synth
+    from exq_amd.kernels import fused_experts, fused_experts_mixed
+    from exq_amd.kernels.fused_moe import moe_workspace_bytes
+    T, seed = {"deepseek_v2_lite": (2048, 3), "mixtral": (4096, 4)}[name]
+    cfg = synth.CONFIGS[name]
+    x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, seed)).to(torch.bfloat16).to(dev)
+    ids, w = synth.routing(cfg, T, 0)
+    tid = torch.from_numpy(ids.astype(np.int32)).to(dev)
+    tw = torch.from_numpy(w).to(dev)
+    ws = torch.zeros(moe_workspace_bytes(T, cfg.hidden, cfg.inter, cfg.n_experts, cfg.top_k,
+                                         cfg.n_shared), dtype=torch.uint8, device=dev)
+    flops = 2.0 * T * (cfg.top_k + cfg.n_shared) * 3 * cfg.hidden * cfg.inter
+    if name == "deepseek_v2_lite":
+        bank = weights if weights is not None else _deepseek_bank(cfg, 0, dev)
+        return name, T, lambda: fused_experts_mixed(x, bank, tw, tid, workspace=ws), flops
+    p13, s13, p2, s2 = weights if weights is not None else _int4_layer(cfg, 0, dev)
+    return name, T, lambda: fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws), flops
+
+
+def prefill_rows(calls, reps):
+    rows = []
+    for name, T, fn, flops in calls:
+        ms = _graph_time(fn, reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        rows.append({"config": name, "batch": T, "us_per_layer": round(ms * 1e3, 1),
+                     "tokens_per_s": round(T / (ms * 1e-3)), "TFLOPs": round(tf, 1),
+                     "frac_of_mfma_peak": round(tf / MFMA_PEAK_BF16_TFLOPS, 4)})
+        log(f"config {name} prefill T={T}: {ms * 1e3:.1f} us/layer, {tf:.1f} TFLOP/s")
+    return rows
+
+
 def measure_configs(dev, reps):
     """The other BASELINE.json configurations: decode µs/layer and achieved GB/s
     on activated-expert bytes (weights + scales; shared experts included) over
@@ -267,14 +328,6 @@ def measure_configs(dev, reps):
                      "us_per_layer": round(us, 2), "tokens_per_s": round(T / (us * 1e-6)),
                      "achieved_GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)})
         log(f"config {name} T={T}: {us:.2f} us/layer, {gbps:.0f} GB/s")
-
-    def prefill_row(name, T, fn, flops):
-        ms = _graph_time(fn, max(3, reps // 10))
-        tf = flops / (ms * 1e-3) / 1e12
-        rows.append({"config": name, "batch": T, "us_per_layer": round(ms * 1e3, 1),
-                     "tokens_per_s": round(T / (ms * 1e-3)), "TFLOPs": round(tf, 1),
-                     "frac_of_mfma_peak": round(tf / MFMA_PEAK_BF16_TFLOPS, 4)})
-        log(f"config {name} prefill T={T}: {ms * 1e3:.1f} us/layer, {tf:.1f} TFLOP/s")
 
     def routing_for(cfg, T, layer):
         ids, w = synth.routing(cfg, T, layer)
@@ -354,13 +407,7 @@ def measure_configs(dev, reps):
             calls.append(lambda bank=bank, tw=tw, tid=tid, x=x, ws=ws:
                          fused_experts_mixed(x, bank, tw, tid, workspace=ws))
         decode_row("deepseek_v2_lite", cfg, T, calls, nbytes / len(banks), len(banks))
-    T = 2048
-    x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 3)).to(torch.bfloat16).to(dev)
-    tid, tw, _ = routing_for(cfg, T, 0)
-    ws = ws_for(cfg, T)
-    flops = 2.0 * T * (cfg.top_k + cfg.n_shared) * 3 * cfg.hidden * cfg.inter
-    prefill_row("deepseek_v2_lite", T,
-                lambda: fused_experts_mixed(x, banks[0], tw, tid, workspace=ws), flops)
+    rows += prefill_rows([_prefill_call(dev, "deepseek_v2_lite", banks[0])], max(3, reps // 10))
     del banks
     torch.cuda.empty_cache()
 
@@ -378,14 +425,7 @@ def measure_configs(dev, reps):
             calls.append(lambda p13=p13, s13=s13, p2=p2, s2=s2, tw=tw, tid=tid, x=x, ws=ws:
                          fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws))
         decode_row("mixtral", cfg, T, calls, nbytes / len(layers), len(layers))
-    T = 4096
-    x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 4)).to(torch.bfloat16).to(dev)
-    tid, tw, _ = routing_for(cfg, T, 0)
-    p13, s13, p2, s2 = layers[0]
-    ws = ws_for(cfg, T)
-    flops = 2.0 * T * cfg.top_k * 3 * cfg.hidden * cfg.inter
-    prefill_row("mixtral", T, lambda: fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws),
-                flops)
+    rows += prefill_rows([_prefill_call(dev, "mixtral", layers[0])], max(3, reps // 10))
     del layers
     torch.cuda.empty_cache()
     return rows
@@ -438,6 +478,21 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     cfg = synth.CONFIGS["qwen3"]
+    if args.prefill_only:  # the MFMA-path configurations alone (profiles, counter runs)
+        rows = []
+        for name in ("deepseek_v2_lite", "mixtral"):
+            call = _prefill_call(dev, name)
+            if args.eager:
+                call[2]()
+                torch.cuda.synchronize()
+                log(f"{name} prefill: one eager call")
+            else:
+                rows += prefill_rows([call], max(3, args.steps // 10))
+            del call
+            torch.cuda.empty_cache()
+        if rows:
+            print(json.dumps({"prefill": rows}), flush=True)
+        return
     if args.pmc_run:
         src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)

@@ -368,19 +368,24 @@ __global__ void __launch_bounds__(NTH, 2) moe_gemm_kernel(GemmArgs a) {
   // XCD-aware order: work-group i runs on XCD i % 8, so each XCD takes a
   // contiguous range of units and neighbouring blocks of one token group
   // (which share the staged activations) stay in one L2.
+  // A grid smaller than 8 * per (when only the INT8 groups are left here)
+  // strides over the order.
   const int per = (U + 7) >> 3;
-  const int local = blockIdx.x >> 3;
-  const int unit = (blockIdx.x & 7) * per + local;
-  if (local >= per || unit >= U) return;
-  const int tgi = unit / a.n_blocks;
-  const int blk = unit - tgi * a.n_blocks;
-  const TgEntry te = a.tg[lo + tgi];
-  if (te.tier == 0) {
-    gemm_body<0, BF, MODE>(a, te, blk, lds);
-  } else if (te.tier == 1) {
-    gemm_body<1, BF, MODE>(a, te, blk, lds);
-  } else {
-    gemm_body<2, BF, MODE>(a, te, blk, lds);
+  for (int idx = blockIdx.x; idx < 8 * per; idx += gridDim.x) {
+    const int local = idx >> 3;
+    const int unit = (idx & 7) * per + local;
+    if (unit >= U) continue;
+    const int tgi = unit / a.n_blocks;
+    const int blk = unit - tgi * a.n_blocks;
+    const TgEntry te = a.tg[lo + tgi];
+    if (te.tier == 0) {
+      gemm_body<0, BF, MODE>(a, te, blk, lds);
+    } else if (te.tier == 1) {
+      gemm_body<1, BF, MODE>(a, te, blk, lds);
+    } else {
+      gemm_body<2, BF, MODE>(a, te, blk, lds);
+    }
+    __syncthreads();  // the staged rows and partial tiles of this unit are dead
   }
 }
 
@@ -421,7 +426,10 @@ __global__ void __launch_bounds__(256) combine_partials_kernel(
 
 template <int MODE>
 int launch_gemm(bool bf, const GemmArgs& a, int64_t units_cap, hipStream_t s) {
-  const int64_t grid = 8 * cdiv(units_cap, 8);
+  int64_t grid = 8 * cdiv(units_cap, 8);
+  // With the tiled kernels running, only INT8 groups (if any) are left here:
+  // a resident-sized grid strides over them instead of launching the cap.
+  if ((a.skip_i4 || a.skip_bf) && grid > 2048) grid = 2048;
   if (grid <= 0) return EXQ_SUCCESS;
   if (grid > INT32_MAX)
     return set_error(EXQ_ERROR_UNSUPPORTED, "moe_gemm: grid of %lld work-groups too large",

@@ -150,3 +150,26 @@ def test_prefill_sorted_bf16_gemm_tiled(dtype, device):
     Wm[3] = 0
     ref = moe.grouped_gemm_sorted(a, Wm, r_ends)
     assert_close_rel(out, ref, TOL, f"grouped gemm tiled {dtype}")
+
+
+def test_prefill_mixed_mostly_int8_strided_grid(device):
+    """Mostly INT8 experts next to INT4 and BF16 ones at a large batch: the
+    grouped kernel's grid (capped while the tiled kernels run) strides over
+    more units than it has work-groups."""
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    banner("prefill mixed mostly int8")
+    T, E = 2000, 16
+    cfg = synth.MoeConfig("mix_int8", 46, 512, 512, E, 4, False)
+    w13, w2 = synth.expert_weights_gpu(E, 512, 512, 72, device)
+    tiers = [1] * E
+    tiers[3] = 2
+    tiers[9] = 0
+    bank = MixedExpertBank.from_weights(w13, w2, tiers)
+    ids, w = synth.routing(cfg, T)
+    int8_rows = sum(int((ids == e).sum()) for e in range(E) if tiers[e] == 1)
+    assert int8_rows // 64 * (512 // 16) > 2048  # more gate/up units than the capped grid
+    x = _hidden(T, 512, 950, device, torch.bfloat16)
+    out = fused_experts_mixed(x, bank, torch.from_numpy(w).to(device),
+                              torch.from_numpy(ids).to(device))
+    from tests.test_gpu_mixed import _oracle
+    assert_close_rel(out, _oracle(bank, x, ids, w), TOL, "prefill mixed mostly int8")
