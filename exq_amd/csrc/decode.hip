@@ -67,8 +67,11 @@ __host__ __device__ constexpr int rows_b(int nt) { return nt == 1 ? 64 : 32; }
 __host__ __device__ constexpr int ring_regs(int nt) { return nt == 1 ? 12 : 20; }
 
 // LDS bytes per wave: the INT4 weight slice of the DMA path and, after a
-// pass's k-loop, the wave's partial tiles.
-constexpr int WAVE_LDS = 8192;
+// pass's k-loop, the wave's partial tiles (WAVE_W), then the unit's fp16
+// group scales (WAVE_S).
+constexpr int WAVE_W = 8192;
+constexpr int WAVE_S = 1024;
+constexpr int WAVE_LDS = WAVE_W + WAVE_S;
 
 struct Proj {
   const uint16_t* bf16;
@@ -339,8 +342,8 @@ struct Geo {
   static constexpr int P0 = ring_regs(NT) / SLOT;
   static constexpr int P = P0 < 1 ? 1 : (P0 > 4 ? 4 : P0);          // ring depth (k-blocks)
   static constexpr int KBSTRIDE = TIER == 2 ? 64 : (TIER == 1 ? 128 : 256);  // row bytes per k-block
-  static constexpr int CK = WAVE_LDS / (RS * 1024);                 // INT4 k-blocks a wave holds in LDS
-  static_assert(RS * NT * 1024 <= WAVE_LDS, "partial tiles exceed the wave's LDS region");
+  static constexpr int CK = WAVE_W / (RS * 1024);                   // INT4 k-blocks a wave holds in LDS
+  static_assert(RS * NT * 1024 <= WAVE_W, "partial tiles exceed the wave's LDS region");
 };
 
 // Per-unit quantities shared by both k-loop variants.
@@ -587,15 +590,29 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
   };
 
   dma();
+  // The unit's fp16 group scales in one instruction: its rows' scales are one
+  // contiguous block (two for gate/up: the gate rows and the up rows), copied
+  // whole into the wave's scale area (scattered 2-byte loads cost several
+  // times a 1 KiB load in the vector-memory pipeline).
+  {
+    const int blk_bytes = 16 * u.ng * 2;  // 16 rows
+    int goff;
+    if constexpr (PH == 0) {
+      const int half = u.lane * 16 < blk_bytes ? 0 : 1;
+      goff = (half ? a.I + blk * 16 : blk * 16) * u.ng * 2 + u.lane * 16 - half * blk_bytes;
+    } else {
+      goff = blk * G::ROWS_B * u.ng * 2 + u.lane * 16;
+    }
+    const bool in = u.lane * 16 < RS * blk_bytes;
+    dma16(in ? u.sr : u.snull, region + WAVE_W, in ? goff : 0);
+  }
   int sl[NT];
   const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, 0, sl));
 
   const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
   asm volatile("" : "+v"(dq_magic));  // keep the magic in a VGPR: one v_and_or_b32 per pair
-  int soff[RS];
-#pragma unroll
-  for (int rs = 0; rs < RS; ++rs) soff[rs] = u.row(a, blk, rs * 16 + u.r16) * u.ng * 2;
+  const uint16_t* sc_lds = reinterpret_cast<const uint16_t*>(region + WAVE_W);
 
   for (int r0 = 0; r0 < cnt; r0 += NT * 16) {
     const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
@@ -608,14 +625,9 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) xo[tt] = u.xoff(a, sl[tt]);
     uint4 areg[DA][4 * NT];
-    uint32_t sreg[DA][RS];
     auto load_a = [&](int p, int kbl) {  // zeros past the wave's range
       const bool ok = kbl < u.nmy;
       const int kb = ok ? u.lo + kbl : u.lo;
-#pragma unroll
-      for (int rs = 0; rs < RS; ++rs)
-        sreg[p][rs] = __builtin_amdgcn_raw_buffer_load_b16(ok ? u.sr : u.snull, soff[rs],
-                                                           (kb >> a.gshift) * 2, 0);
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -649,7 +661,12 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
             acc = dmfma<BF>(xa[1], ddeq4(w.y, dq_mask, dq_magic), acc);
             acc = dmfma<BF>(xa[2], ddeq4(w.z, dq_mask, dq_magic), acc);
             acc = dmfma<BF>(xa[3], ddeq4(w.w, dq_mask, dq_magic), acc);
-            tot[rs][tt] += f16_bits_to_f32(sreg[p][rs]) * acc;
+            // past the wave's range the activations (and so acc) are zero
+            const float sc =
+                kbl < u.nmy
+                    ? f16_bits_to_f32(sc_lds[(rs * 16 + u.r16) * u.ng + ((u.lo + kbl) >> a.gshift)])
+                    : 0.f;
+            tot[rs][tt] += sc * acc;
           }
         }
       }
@@ -960,7 +977,9 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     // INT4 slices go through LDS when every wave's k-range fits its region
     const int rs = ph == 0 ? 2 : rows_b(nt) / 16;
     const int nkb = (ph == 0 ? d.H : d.I) / 128;
-    const bool dma = (nkb + 3) / 4 <= WAVE_LDS / (rs * 1024);
+    const int ng = nkb >> a.gshift;
+    // the wave's k-range fits its weight region and the unit's scales its scale area
+    const bool dma = (nkb + 3) / 4 <= WAVE_W / (rs * 1024) && rs * 16 * ng * 2 <= WAVE_S;
     const decode_kernel_t kern = pick_kernel(d.bf, ph, mixed, dma);
     const int64_t units = max_active * (ph == 0 ? a.nbA : a.nbB);
     int resident = 0;
