@@ -72,6 +72,10 @@ __host__ __device__ constexpr int ring_regs(int nt) { return nt == 1 ? 12 : 20; 
 constexpr int WAVE_W = 8192;
 constexpr int WAVE_S = 1024;
 constexpr int WAVE_LDS = WAVE_W + WAVE_S;
+// Register-ring units keep their k-range's group scales behind the partial
+// tiles (at most 4 KiB), in the rest of the wave's region.
+constexpr int SCALE_OFF = 4096;
+constexpr int RING_SCALE_BYTES = WAVE_LDS - SCALE_OFF;
 
 struct Proj {
   const uint16_t* bf16;
@@ -209,6 +213,18 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* l
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)lds, 16, voff, 0, 0, 0);
 #endif
+}
+
+// 4 bytes per lane into LDS at lds + 4 * lane (buffer_load_dword ... lds).
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)lds, 4, voff, 0, 0, 0);
+#endif
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm_le() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 // Buffer resource over `bytes` bytes at `base` (gfx9 word 3): loads beyond
@@ -700,19 +716,43 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
   using G = Geo<TIER, PH, NT>;
   constexpr int RS = G::RS, QPK = G::QPK, P = G::P, WSLOT = G::WSLOT;
   const UnitCtx<TIER, PH, NT> u(a, e, blk);
-  int voff[RS], soff[RS];
+  int voff[RS];
 #pragma unroll
-  for (int rs = 0; rs < RS; ++rs) {
-    const int row = u.row(a, blk, rs * 16 + u.r16);
-    voff[rs] = row * u.rowbytes + u.kq * 16 * QPK;
-    soff[rs] = row * u.ng * 2;
-  }
+  for (int rs = 0; rs < RS; ++rs)
+    voff[rs] = u.row(a, blk, rs * 16 + u.r16) * u.rowbytes + u.kq * 16 * QPK;
   const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
   asm volatile("" : "+v"(dq_magic));
 
+  // INT4 group scales of the wave's k-range, copied into LDS behind the
+  // partial-tile area with 4-byte LDS-DMA instructions (row r's groups
+  // g_lo.. as nd dwords from its aligned start) before the ring loads, so the
+  // k-loop reads them from LDS instead of issuing scattered 2-byte loads.
+  const int g_lo = u.lo >> a.gshift;
+  const int ngw = u.nmy > 0 ? ((u.lo + u.nmy - 1) >> a.gshift) - g_lo + 1 : 1;
+  const int nd = (ngw * 2 + 2 + 3) >> 2;  // dwords per row (2 bytes of alignment slack)
+  const uint16_t* sc_lds = reinterpret_cast<const uint16_t*>(lds + u.wave * WAVE_LDS + SCALE_OFF);
+  if constexpr (TIER == 2) {
+    unsigned char* dst = lds + u.wave * WAVE_LDS + SCALE_OFF;
+    const int nflat = RS * 16 * nd;
+    for (int i0 = 0; i0 < nflat; i0 += 64) {  // wave-uniform trip count
+      const int f = i0 + u.lane;
+      const int rr = f / nd, d = f - (f / nd) * nd;
+      const bool in = f < nflat;
+      const int b0 = (u.row(a, blk, in ? rr : 0) * u.ng + g_lo) * 2;
+      dma4(in ? u.sr : u.snull, dst + i0 * 4, in ? (b0 & ~3) + d * 4 : 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the copies go out before the ring loads
+  }
+  // scale of row-set row rs*16 + r16, k-block kb (in the wave's range)
+  auto scale_at = [&](int rs, int kb) {
+    const int row = u.row(a, blk, rs * 16 + u.r16);
+    const int e0 = ((row * u.ng + g_lo) * 2) & 2;
+    return f16_bits_to_f32(
+        sc_lds[((rs * 16 + u.r16) * nd * 4 + e0) / 2 + ((kb >> a.gshift) - g_lo)]);
+  };
+
   uint4 wreg[P][WSLOT];
-  uint32_t sreg[P][RS];
   uint4 areg[P][4 * NT];
   int xo[NT];
   auto load_w = [&](int p, int kbl) {
@@ -725,9 +765,6 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
       for (int h = 0; h < QPK; ++h)
         wreg[p][rs * QPK + h] = __builtin_bit_cast(
             uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff[rs] + h * 16, kb * G::KBSTRIDE, 0));
-      if constexpr (TIER == 2)
-        sreg[p][rs] = __builtin_amdgcn_raw_buffer_load_b16(ok ? u.sr : u.snull, soff[rs],
-                                                           (kb >> a.gshift) * 2, 0);
     }
   };
   auto load_a = [&](int p, int kbl) {
@@ -765,6 +802,10 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
     for (int rs = 0; rs < RS; ++rs)
 #pragma unroll
       for (int t = 0; t < NT; ++t) tot[rs][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // the scale copies were issued before every ring load now outstanding
+    if constexpr (TIER == 2) {
+      if (r0 == 0) wait_vm_le<P * (RS * QPK + 4 * NT)>();
+    }
 
     for (int kb0 = 0; kb0 < u.nmy; kb0 += P) {
 #pragma unroll
@@ -778,7 +819,8 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
             bfr[1] = ddeq4(w.y, dq_mask, dq_magic);
             bfr[2] = ddeq4(w.z, dq_mask, dq_magic);
             bfr[3] = ddeq4(w.w, dq_mask, dq_magic);
-            sc = f16_bits_to_f32(sreg[p][rs]);
+            // past the wave's range the activations (so acc) are zero
+            sc = kb0 + p < u.nmy ? scale_at(rs, u.lo + kb0 + p) : 0.f;
           } else if constexpr (TIER == 1) {
             const uint4 w0 = wreg[p][rs * QPK + 0], w1 = wreg[p][rs * QPK + 1];
             const uint2 d0 = ddeq8<BF>(w0.x), d1 = ddeq8<BF>(w0.y);
@@ -940,11 +982,18 @@ int resident_work_groups(const void* kern, int threads, size_t lds, int* out) {
 }
 
 bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, int64_t H,
-                           int64_t group_size) {
+                           int64_t I, int64_t group_size) {
   const int64_t gkb = group_size / 128;  // k-blocks per scale group: a power of two
-  return T >= 1 && T <= 64 && T * k <= MAX_SLOTS && Ep <= kDecodeMaxBuckets &&
-         n_shared <= 64 && H / 32 <= kDecodeMaxHBlocks && H % 64 == 0 && gkb >= 1 &&
-         (gkb & (gkb - 1)) == 0;
+  if (!(T >= 1 && T <= 64 && T * k <= MAX_SLOTS && Ep <= kDecodeMaxBuckets && n_shared <= 64 &&
+        H / 32 <= kDecodeMaxHBlocks && H % 64 == 0 && gkb >= 1 && (gkb & (gkb - 1)) == 0))
+    return false;
+  // a register-ring unit's scales (rows x dwords of its widest k-range) fit in LDS
+  auto ring_scales_fit = [&](int64_t K, int64_t rows) {
+    const int64_t nkb = K / 128, span = (nkb + 3) / 4;
+    const int64_t ngw = (span + gkb - 1) / gkb + 1;
+    return rows * ((ngw * 2 + 2 + 3) / 4) * 4 <= RING_SCALE_BYTES;
+  };
+  return ring_scales_fit(H, 32) && ring_scales_fit(I, rows_b(1));
 }
 
 int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {

@@ -144,7 +144,7 @@ struct DecodeLaunch {
 };
 
 bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, int64_t H,
-                           int64_t group_size);
+                           int64_t I, int64_t group_size);
 int launch_decode_layer(const DecodeLaunch& d, hipStream_t s);
 
 // The four stage events installed with exq_set_stage_events for the current

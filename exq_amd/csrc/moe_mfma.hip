@@ -575,7 +575,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     ~HookReset() { g_stage_events_set = false; }
   } hook_reset;
   const bool decode =
-      decode_path_supported(T, k, Ep, p->n_shared, p->hidden_size, p->group_size);
+      decode_path_supported(T, k, Ep, p->n_shared, p->hidden_size, p->inter_size, p->group_size);
   int st = EXQ_SUCCESS;
   if (!decode) {
     st = record_stage(0, s);
