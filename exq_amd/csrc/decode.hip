@@ -101,6 +101,7 @@ struct LayerArgs {
   uint16_t* out;                // [T, H]
   int* sync;                    // combine counters, see sync_* below
   int nbA, nbB;                 // units per expert: I / 16, H / rows_b(NT)
+  int nsplit;                   // down: k-splits per (expert, row block), partial sets
 };
 
 // Counter layout of the sync region (fixed, independent of the problem size):
@@ -199,8 +200,12 @@ __device__ __forceinline__ void wave_lds_fence() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's LDS ops have completed
 }
 
+// The builtin wait tells the compiler's own wait insertion that nothing is in
+// flight any more (so it adds no waits of its own for older loads later);
+// the empty asm keeps memory accesses on their side of it.
 __device__ __forceinline__ void wait_vm_all() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // loads, stores and LDS DMA have landed
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): loads, stores and LDS DMA have landed
+  asm volatile("" ::: "memory");
 }
 
 typedef void __attribute__((address_space(3)))* lptr_t;
@@ -371,15 +376,20 @@ struct UnitCtx {
   __amdgpu_buffer_rsrc_t wr, wnull, sr, snull, xr, xnull, part_r;
   float rowscale[G::RS];
 
-  __device__ __forceinline__ UnitCtx(const LayerArgs& a, int e, int blk) {
+  int split;  // down: this unit's k-split (its partial set)
+  __device__ __forceinline__ UnitCtx(const LayerArgs& a, int e, int blk, int sp = 0) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     r16 = lane & 15;
     kq = lane >> 4;
     K = PH == 0 ? a.H : a.I;
     nkb = K >> 7;
-    lo = (wave * nkb) >> 2;
-    nmy = (((wave + 1) * nkb) >> 2) - lo;  // k-blocks of this wave
+    split = sp;
+    // the split's k-blocks [s0, s1), then this wave's quarter of them
+    const int ns = PH == 0 ? 1 : a.nsplit;
+    const int s0 = (sp * nkb) / ns, s1 = ((sp + 1) * nkb) / ns;
+    lo = s0 + ((wave * (s1 - s0)) >> 2);
+    nmy = s0 + (((wave + 1) * (s1 - s0)) >> 2) - lo;  // k-blocks of this wave
     const Proj& W = PH == 0 ? a.w13 : a.w2;
     const int n_rows = PH == 0 ? 2 * a.I : a.H;
     const int widx = a.index ? __builtin_amdgcn_readfirstlane(a.index[e]) : e;
@@ -398,7 +408,7 @@ struct UnitCtx {
     xr = PH == 0 ? make_rsrc(a.x, (int64_t)a.T * a.H * 2)
                  : make_rsrc(a.mid, (int64_t)a.T * a.kp * a.I * 2);
     xnull = make_rsrc(PH == 0 ? (const void*)a.x : (const void*)a.mid, 0);
-    part_r = make_rsrc(a.part, (int64_t)a.T * a.kp * a.H * 4);
+    part_r = make_rsrc(a.part, (int64_t)a.nsplit * a.T * a.kp * a.H * 4);
 #pragma unroll
     for (int rs = 0; rs < G::RS; ++rs) {
       rowscale[rs] = 1.f;
@@ -501,7 +511,8 @@ __device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TI
         if (q < cc)
           __builtin_amdgcn_raw_buffer_store_b32(
               __builtin_bit_cast(uint32_t, s[i] * rsc), u.part_r,
-              (slot * a.H + blk * ROWS_B + rs * 16 + u.r16) * 4, 0, CPOL_SC1);
+              ((u.split * a.T * a.kp + slot) * a.H + blk * ROWS_B + rs * 16 + u.r16) * 4, 0,
+              CPOL_SC1);
       }
       stored = true;
     }
@@ -517,13 +528,14 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
   if (threadIdx.x == 0) {
     const int old =
         __hip_atomic_fetch_add(sync_c(a, blk), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = old == n_active - 1;
+    *s_flag = old == n_active * a.nsplit - 1;
   }
   __syncthreads();
   if (!*s_flag) return;
   // out[t, h..h+3] = sum over the token's slots j (ascending) of weight *
   // partial; a chunk of eight slots' loads is issued at once
-  const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, (int64_t)a.T * a.kp * a.H * 4);
+  const int64_t set = (int64_t)a.T * a.kp * a.H;  // floats per partial set
+  const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, a.nsplit * set * 4);
   const __amdgpu_buffer_rsrc_t part_null = make_rsrc(a.part, 0);
   const int h0 = blk * ROWS_B;
   for (int idx = threadIdx.x; idx < a.T * (ROWS_B / 4); idx += DNT) {
@@ -547,6 +559,15 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
             float4, __builtin_amdgcn_raw_buffer_load_b128(
                         ok ? part_r : part_null, ok ? ((t * a.kp + j) * a.H + h) * 4 : 0, 0,
                         CPOL_SC1));
+        // further k-splits of the same row, in split order
+        for (int sp = 1; sp < a.nsplit; ++sp) {
+          const float4 q = __builtin_bit_cast(
+              float4, __builtin_amdgcn_raw_buffer_load_b128(
+                          ok ? part_r : part_null,
+                          ok ? (int)((sp * set + (int64_t)(t * a.kp + j) * a.H + h) * 4) : 0, 0,
+                          CPOL_SC1));
+          pv[jj].x += q.x; pv[jj].y += q.y; pv[jj].z += q.z; pv[jj].w += q.w;
+        }
       }
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
@@ -583,11 +604,11 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
 // register ring.
 template <bool BF, int PH, int NT>
 __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt, int e, int blk,
-                                             unsigned char* lds) {
+                                             int sp, unsigned char* lds) {
   using G = Geo<2, PH, NT>;
   constexpr int RS = G::RS, CK = G::CK;
   constexpr int DA = NT == 4 ? 1 : 2;  // activation k-blocks in flight
-  const UnitCtx<2, PH, NT> u(a, e, blk);
+  const UnitCtx<2, PH, NT> u(a, e, blk, sp);
   unsigned char* region = lds + u.wave * WAVE_LDS;
   const int p4 = 4 * u.nmy;                 // 16-byte pieces per row in LDS
   const int xm = (u.nmy & 1) ? 3 : 7;       // swizzle mask keeps c ^ (rr & xm) < p4
@@ -686,7 +707,7 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
           }
         }
       }
-      load_a(p, kbl + DA);
+      if (kbl + DA < CK) load_a(p, kbl + DA);
     }
     // partial tiles into this wave's own region (its weight reads are done)
     float4* red = reinterpret_cast<float4*>(region);
@@ -712,10 +733,10 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
 // ring fill of weights is issued before the expert's rows are gathered.
 template <int TIER, bool BF, int PH, int NT>
 __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& rt, int e, int blk,
-                                              unsigned char* lds) {
+                                              int sp, unsigned char* lds) {
   using G = Geo<TIER, PH, NT>;
   constexpr int RS = G::RS, QPK = G::QPK, P = G::P, WSLOT = G::WSLOT;
-  const UnitCtx<TIER, PH, NT> u(a, e, blk);
+  const UnitCtx<TIER, PH, NT> u(a, e, blk, sp);
   int voff[RS];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs)
@@ -895,8 +916,10 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
 // A grid of at most one resident round of work-groups; each routes once and
 // then takes units blockIdx.x, blockIdx.x + gridDim.x, ... (expert-major:
 // unit u is row block u % nb of the (u / nb)-th active expert).
+// Four waves per SIMD (four work-groups per CU, at most 128 VGPRs) except
+// the mixed-tier down kernel, whose register use needs two.
 template <bool BF, int PH, int NT, bool MIXED, bool DMA>
-__global__ void __launch_bounds__(DNT, 2) moe_decode_kernel(LayerArgs a) {
+__global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_kernel(LayerArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
   __shared__ Route rt;
   __shared__ int s_flag;
@@ -913,23 +936,26 @@ __global__ void __launch_bounds__(DNT, 2) moe_decode_kernel(LayerArgs a) {
     }
     return;
   }
-  const int nb = PH == 0 ? a.nbA : a.nbB;
+  // unit u = (active expert, row block, k-split), the split fastest
+  const int ns = PH == 0 ? 1 : a.nsplit;
+  const int nb = (PH == 0 ? a.nbA : a.nbB) * ns;
   const int n_units = n_active * nb;
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {  // uniform across the work-group
     const int ai = u / nb;
-    const int blk = u - ai * nb;
+    const int bs = u - ai * nb;
+    const int blk = bs / ns, sp = bs - (bs / ns) * ns;
     const int e = select_expert(ai, word, incl, c);
     const int tier = MIXED ? __builtin_amdgcn_readfirstlane((int)a.tier[e]) : 2;
     if (!MIXED || tier == 2) {
       if constexpr (DMA)
-        run_unit_dma<BF, PH, NT>(a, rt, e, blk, dyn_lds);
+        run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
       else
-        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, dyn_lds);
+        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
     } else if constexpr (MIXED) {
       if (tier == 1)
-        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, dyn_lds);
+        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
       else
-        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, dyn_lds);
+        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
     }
     if constexpr (PH == 1) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_active, &s_flag);
   }
@@ -1020,17 +1046,35 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   const int nt = 1;
   a.nbA = d.I / 16;
   a.nbB = d.H / rows_b(nt);
+  a.nsplit = 1;
   const int64_t max_active = (int64_t)(d.T * d.k < d.E ? d.T * d.k : d.E) + (d.Ep - d.E);
   for (int ph = 0; ph < 2; ++ph) {
     const size_t lds = (size_t)DW * WAVE_LDS;  // per-wave weight slices / partial tiles
+    if (ph == 1) {
+      // Few down units (large experts, few active): split each (expert, row
+      // block) contraction over up to kDecodeMaxSplit work-groups, each with
+      // at least four k-blocks, to fill the resident round.
+      int resident = 0;
+      const int st = resident_work_groups(
+          reinterpret_cast<const void*>(pick_kernel(d.bf, 1, mixed, false)), DNT, lds, &resident);
+      if (st) return st;
+      const int64_t u1 = max_active * a.nbB;
+      int64_t sp = u1 > 0 ? resident / u1 : 1;
+      const int64_t cap = (d.I / 128) / 4;
+      if (sp > cap) sp = cap;
+      if (sp > kDecodeMaxSplit) sp = kDecodeMaxSplit;
+      a.nsplit = sp < 1 ? 1 : (int)sp;
+    }
     // INT4 slices go through LDS when every wave's k-range fits its region
     const int rs = ph == 0 ? 2 : rows_b(nt) / 16;
     const int nkb = (ph == 0 ? d.H : d.I) / 128;
-    const int ng = nkb >> a.gshift;
+    const int ns = ph == 0 ? 1 : a.nsplit;
+    const int nkb_split = (nkb + ns - 1) / ns;  // the widest split
+    const int ng = nkb >> a.gshift;             // the unit's whole scale rows are copied
     // the wave's k-range fits its weight region and the unit's scales its scale area
-    const bool dma = (nkb + 3) / 4 <= WAVE_W / (rs * 1024) && rs * 16 * ng * 2 <= WAVE_S;
+    const bool dma = (nkb_split + 3) / 4 <= WAVE_W / (rs * 1024) && rs * 16 * ng * 2 <= WAVE_S;
     const decode_kernel_t kern = pick_kernel(d.bf, ph, mixed, dma);
-    const int64_t units = max_active * (ph == 0 ? a.nbA : a.nbB);
+    const int64_t units = max_active * (ph == 0 ? a.nbA : (int64_t)a.nbB * a.nsplit);
     int resident = 0;
     const int st0 = resident_work_groups(reinterpret_cast<const void*>(kern), DNT, lds, &resident);
     if (st0) return st0;

@@ -115,6 +115,9 @@ int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, 
 constexpr int kDecodeMaxBuckets = 1024;   // routed + shared experts
 constexpr int kDecodeMaxHBlocks = 512;    // H / 64
 constexpr size_t kDecodeSyncBytes = (size_t)(kDecodeMaxBuckets + kDecodeMaxHBlocks + 2) * 128;
+// The down kernel may split each contraction over this many work-groups; the
+// fused workspace holds one fp32 partial set per split.
+constexpr int kDecodeMaxSplit = 8;
 
 struct DecodeLaunch {
   const void* ids;
@@ -137,7 +140,7 @@ struct DecodeLaunch {
   const int32_t* index;    // [Ep] or null
   int H, I, group_size;
   uint16_t* mid;           // [T * kp, I]
-  float* part;             // [T * kp, H]
+  float* part;             // [kDecodeMaxSplit][T * kp, H]
   uint16_t* out;           // [T, H]
   int* sync;
   bool bf;

@@ -481,7 +481,11 @@ FusedLayout fused_layout(const exq_moe_problem& p) {
   L.sorted = off;   off = align_up(off + (size_t)L.n * 4, 256);
   L.tg = off;       off = align_up(off + (size_t)L.tg_cap * sizeof(TgEntry), 256);
   L.mid = off;      off = align_up(off + (size_t)L.n * p.inter_size * 2, 256);
-  L.partial = off;  off = align_up(off + (size_t)L.n * p.hidden_size * 4, 256);
+  // decode batches: one partial set per down k-split
+  const bool dec = decode_path_supported(p.n_tokens, p.top_k, p.n_experts + p.n_shared,
+                                         p.n_shared, p.hidden_size, p.inter_size, p.group_size);
+  L.partial = off;
+  off = align_up(off + (size_t)L.n * p.hidden_size * 4 * (dec ? kDecodeMaxSplit : 1), 256);
   // group row sums of the tiled prefill kernel: x rows (GATEUP), then mid rows (DOWN)
   const int64_t rs_x = tile_rowsum_floats(p.n_tokens, p.hidden_size);
   const int64_t rs_mid = tile_rowsum_floats(L.n, p.inter_size);

@@ -165,6 +165,28 @@ def test_fused_long_contraction_multi_round(device):
         assert_close_rel(out, ref, TOL, f"long K T={T}")
 
 
+@pytest.mark.parametrize("name,H,I,E,k,T", [("olmoe_t1", 2048, 1024, 64, 8, 1),
+                                             ("uneven_split", 256, 1664, 4, 1, 1),
+                                             ("uneven_split_t2", 256, 1664, 4, 1, 2)])
+def test_fused_down_split_contraction(name, H, I, E, k, T, device):
+    """Few active experts leave the down projection short of work-groups, so
+    each contraction is split over several (2 for OLMoE at T=1; 3 uneven
+    splits of 13 k-blocks here) and the splits are summed in a fixed order:
+    the result matches the oracle and repeats bitwise."""
+    from exq_amd.kernels import fused_experts
+    cfg = synth.MoeConfig(name, 31, H, I, E, k, True, zipf=False)
+    banner(f"fused split {name} T={T}")
+    p13, s13, p2, s2 = _pack_gpu(E, I, H, 600 + I, device)
+    ids, w, tid, tw = _routing(cfg, T, device)
+    for dtype in (torch.bfloat16, torch.float16):
+        x = _hidden(T, H, 7 + T, device).to(dtype)
+        out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+        ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+        assert_close_rel(out, ref, TOL, f"split {name} {dtype}")
+        for _ in range(2):
+            assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid), out)
+
+
 def test_moe_int4_forward_sorted_output(device):
     from exq_amd.kernels import moe_int4_forward, sort_tokens_by_expert
     from oracle import moe

@@ -81,6 +81,31 @@ def test_mixed_olmoe_shape(device):
     assert E == bank.n_experts
 
 
+@pytest.mark.parametrize("T", [1, 2])
+def test_mixed_tiers_split_contraction(T, device):
+    """BF16, INT8 and INT4 down projections with their 13-k-block contraction
+    split three ways (few active experts); fixed-order split sums repeat
+    bitwise."""
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    banner(f"mixed split T={T}")
+    E = 8
+    cfg = synth.MoeConfig("mix_split", 32, 512, 1664, E, 2, True, zipf=False)
+    w13, w2 = synth.expert_weights_gpu(E, 1664, 512, 73, device)
+    tiers = [0, 1, 2, 0, 1, 2, 1, 2]
+    for act in (torch.bfloat16, torch.float16):
+        bank = MixedExpertBank.from_weights(w13, w2, tiers, act_dtype=act)
+        for seed in range(3):  # different expert pairs
+            ids, w = synth.routing(cfg, T)
+            ids = (ids + seed * 3) % E
+            ids[0, :] = [seed % E, (seed + 1) % E]
+            x = torch.from_numpy(synth.hidden_np(T, 512, 40 + seed)).to(act).to(device)
+            tid = torch.from_numpy(ids).to(device)
+            tw = torch.from_numpy(w).to(device)
+            out = fused_experts_mixed(x, bank, tw, tid)
+            assert_close_rel(out, _oracle(bank, x, ids, w), TOL, f"mixed split {act} {seed}")
+            assert torch.equal(fused_experts_mixed(x, bank, tw, tid), out)
+
+
 @pytest.mark.parametrize("T", [1, 16, 64, 200])
 def test_shared_experts_deepseek_shape(T, device):
     from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
