@@ -244,26 +244,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 struct Route {
   uint32_t bitmap[MAX_BM_WORDS];
   int16_t ids[MAX_SLOTS];  // routed id of slot t*k + j (-1: dropped)
+  int multi;               // some expert has more than 16 rows
 };
 
 // Load the ids and build the bitmap (all threads); returns the number of
 // active experts and leaves this lane's bitmap word and prefix for
 // select_expert.
-__device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t& word, int& incl,
-                                     int& c) {
+// Also counts each expert's rows into cntw (16 bits per expert, two per word;
+// a count is at most T * k <= MAX_SLOTS, so no carry crosses a half).
+__device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t* cntw, uint32_t& word,
+                                     int& incl, int& c) {
   const int lane = threadIdx.x & 63;
   const int n = a.T * a.k;
   const int nw = (a.Ep + 31) >> 5;
   if (threadIdx.x < MAX_BM_WORDS) r.bitmap[threadIdx.x] = 0u;
+  if (threadIdx.x == 0) r.multi = a.T > 16 && a.Ep > a.E;  // shared experts take every token
+  for (int i = threadIdx.x; i < (a.Ep + 1) >> 1; i += DNT) cntw[i] = 0u;
   __syncthreads();
   for (int s = threadIdx.x; s < n; s += DNT) {
     const int64_t id = load_index(a.ids, a.ids_dtype, s);
     const int v = (id >= 0 && id < a.E) ? (int)id : -1;
     r.ids[s] = (int16_t)v;
-    if (v >= 0) atomicOr(&r.bitmap[v >> 5], 1u << (v & 31));
+    if (v >= 0) {
+      atomicOr(&r.bitmap[v >> 5], 1u << (v & 31));
+      const uint32_t old = atomicAdd(&cntw[v >> 1], 1u << ((v & 1) * 16));
+      if (((old >> ((v & 1) * 16)) & 0xffffu) >= 16u) r.multi = 1;
+    }
   }
-  if (threadIdx.x < a.Ep - a.E && a.T > 0)
-    atomicOr(&r.bitmap[(a.E + threadIdx.x) >> 5], 1u << ((a.E + threadIdx.x) & 31));
+  if (threadIdx.x < a.Ep - a.E && a.T > 0) {
+    const int v = a.E + threadIdx.x;
+    atomicOr(&r.bitmap[v >> 5], 1u << (v & 31));
+    atomicAdd(&cntw[v >> 1], (uint32_t)a.T << ((v & 1) * 16));
+  }
   __syncthreads();
   word = lane < nw ? r.bitmap[lane] : 0u;
   c = __popc(word);
@@ -309,6 +321,53 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int q) {
   }
   return base;
 }
+
+// Rows of expert e (after route()).
+__device__ __forceinline__ int expert_rows(const uint32_t* cntw, int e) {
+  return (int)((cntw[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+}
+
+// Token tiles (16 rows each) of the active experts, as segments: segment t
+// holds tile t of every expert with more than t tiles, in ascending expert
+// order, so an expert's first tile comes first and its later tiles are
+// spread over other work-groups.  Lane t of the result holds segment t's
+// expert count (lanes past the last segment hold 0); *total = all tiles.
+__device__ __forceinline__ int tile_segments(const LayerArgs& a, const uint32_t* cntw,
+                                             const Route& rt, int* total) {
+  const int lane = threadIdx.x & 63;
+  int seg = 0;
+  for (int e0 = 0; e0 < a.Ep; e0 += 64) {
+    const int e = e0 + lane;
+    const bool act = e < a.Ep && ((rt.bitmap[e >> 5] >> (e & 31)) & 1u);
+    const int nt = act ? (expert_rows(cntw, e) + 15) >> 4 : 0;
+    for (int t = 0; t < 64; ++t) {
+      const uint64_t m = __ballot(nt > t);
+      if (m == 0) break;
+      if (lane == t) seg += __popcll(m);
+    }
+  }
+  int tot = seg;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) tot += __shfl_xor(tot, o, 64);
+  *total = __builtin_amdgcn_readfirstlane(tot);
+  return seg;
+}
+
+// The j-th expert (ascending) with more than t tiles (t >= 1).
+__device__ __forceinline__ int select_tiled_expert(const LayerArgs& a, const uint32_t* cntw,
+                                                   const Route& rt, int t, int j) {
+  const int lane = threadIdx.x & 63;
+  for (int e0 = 0; e0 < a.Ep; e0 += 64) {
+    const int e = e0 + lane;
+    const bool act = e < a.Ep && ((rt.bitmap[e >> 5] >> (e & 31)) & 1u);
+    const uint64_t m = __ballot(act && ((expert_rows(cntw, e) + 15) >> 4) > t);
+    const int cm = __popcll(m);
+    if (j < cm) return e0 + nth_set_bit(m, j);
+    j -= cm;
+  }
+  return 0;  // not reached for j < the segment's count
+}
+
 
 // Expert e's rows (its routed slots t*kp + j in ascending order, the order of
 // the reference's stable sort; every token for a shared expert), found by
@@ -521,14 +580,14 @@ __device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TI
 }
 
 // Down phase, after the unit's last pass: count the unit in for its column
-// block; the last of the block's n_active units combines the block.
+// block; the last of the block's units combines the block.
 template <bool BF, int ROWS_B>
 __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Route& rt, int blk,
-                                                    int n_active, int* s_flag) {
-  if (threadIdx.x == 0) {
+                                                    int n_tiles, int* s_flag) {
+  if (threadIdx.x == 0) {  // n_tiles units (times the k-splits) write each column block
     const int old =
         __hip_atomic_fetch_add(sync_c(a, blk), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = old == n_active * a.nsplit - 1;
+    *s_flag = old == n_tiles * a.nsplit - 1;
   }
   __syncthreads();
   if (!*s_flag) return;
@@ -604,7 +663,7 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
 // register ring.
 template <bool BF, int PH, int NT>
 __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt, int e, int blk,
-                                             int sp, unsigned char* lds) {
+                                             int sp, int tile, unsigned char* lds) {
   using G = Geo<2, PH, NT>;
   constexpr int RS = G::RS, CK = G::CK;
   constexpr int DA = NT == 4 ? 1 : 2;  // activation k-blocks in flight
@@ -643,21 +702,19 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
     const bool in = u.lane * 16 < RS * blk_bytes;
     dma16(in ? u.sr : u.snull, region + WAVE_W, in ? goff : 0);
   }
+  // this unit's rows: tile `tile` of the expert's rows (one pass)
+  const int r_begin = tile * NT * 16;
   int sl[NT];
-  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, 0, sl));
+  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, r_begin, sl));
 
   const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
   asm volatile("" : "+v"(dq_magic));  // keep the magic in a VGPR: one v_and_or_b32 per pair
   const uint16_t* sc_lds = reinterpret_cast<const uint16_t*>(region + WAVE_W);
 
-  for (int r0 = 0; r0 < cnt; r0 += NT * 16) {
+  for (int r0 = r_begin; r0 < cnt && r0 < r_begin + NT * 16; r0 += NT * 16) {
     const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
     const int ntiles = (cc + 15) >> 4;
-    if (r0 > 0) {  // the partial tiles of the previous pass overwrote the slice
-      dma();
-      lane_slots<NT>(a, rt, e, r0, sl);
-    }
     int xo[NT];
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) xo[tt] = u.xoff(a, sl[tt]);
@@ -733,7 +790,7 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
 // ring fill of weights is issued before the expert's rows are gathered.
 template <int TIER, bool BF, int PH, int NT>
 __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& rt, int e, int blk,
-                                              int sp, unsigned char* lds) {
+                                              int sp, int tile, unsigned char* lds) {
   using G = Geo<TIER, PH, NT>;
   constexpr int RS = G::RS, QPK = G::QPK, P = G::P, WSLOT = G::WSLOT;
   const UnitCtx<TIER, PH, NT> u(a, e, blk, sp);
@@ -802,17 +859,14 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
 
 #pragma unroll
   for (int p = 0; p < P; ++p) load_w(p, p);
+  // this unit's rows: tile `tile` of the expert's rows (one pass)
+  const int r_begin = tile * NT * 16;
   int sl[NT];
-  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, 0, sl));
+  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, r_begin, sl));
 
-  for (int r0 = 0; r0 < cnt; r0 += NT * 16) {
+  for (int r0 = r_begin; r0 < cnt && r0 < r_begin + NT * 16; r0 += NT * 16) {
     const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
     const int ntiles = (cc + 15) >> 4;
-    if (r0 > 0) {  // a further pass streams the weights again
-#pragma unroll
-      for (int p = 0; p < P; ++p) load_w(p, p);
-      lane_slots<NT>(a, rt, e, r0, sl);
-    }
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) xo[tt] = u.xoff(a, sl[tt]);
 #pragma unroll
@@ -923,9 +977,10 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
   __shared__ Route rt;
   __shared__ int s_flag;
+  uint32_t* cntw = reinterpret_cast<uint32_t*>(dyn_lds + DW * WAVE_LDS);  // rows per expert
   uint32_t word;
   int incl, c;
-  const int n_active = route(a, rt, word, incl, c);
+  const int n_active = route(a, rt, cntw, word, incl, c);
   if (n_active == 0) {  // nothing routed: the output is zero
     if (PH == 1) {
       uint4* o = reinterpret_cast<uint4*>(a.out);
@@ -936,28 +991,44 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
     }
     return;
   }
-  // unit u = (active expert, row block, k-split), the split fastest
+  // Unit u = (token tile, row block, k-split), the split fastest; tiles in
+  // segments (tile 0 of every active expert, then tile 1 of the experts with
+  // more than 16 rows, ...), so a busy expert's tiles run side by side.
   const int ns = PH == 0 ? 1 : a.nsplit;
   const int nb = (PH == 0 ? a.nbA : a.nbB) * ns;
-  const int n_units = n_active * nb;
+  int n_tiles = n_active;
+  int incl_u = n_active * nb;  // inclusive prefix of the segments' unit counts, lane t = segment t
+  if (rt.multi) {              // (otherwise every expert is one tile: segment 0 only)
+    const int seg = tile_segments(a, cntw, rt, &n_tiles);
+    incl_u = seg * nb;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int v = __shfl_up(incl_u, o, 64);
+      if (lane >= o) incl_u += v;
+    }
+  }
+  const int n_units = n_tiles * nb;
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {  // uniform across the work-group
-    const int ai = u / nb;
-    const int bs = u - ai * nb;
+    const int t = __popcll(__ballot(incl_u <= u));  // segment = tile index
+    const int v = u - (t > 0 ? __builtin_amdgcn_readlane(incl_u, t - 1) : 0);
+    const int ai = v / nb;
+    const int bs = v - ai * nb;
     const int blk = bs / ns, sp = bs - (bs / ns) * ns;
-    const int e = select_expert(ai, word, incl, c);
+    const int e = t == 0 ? select_expert(ai, word, incl, c) : select_tiled_expert(a, cntw, rt, t, ai);
     const int tier = MIXED ? __builtin_amdgcn_readfirstlane((int)a.tier[e]) : 2;
     if (!MIXED || tier == 2) {
       if constexpr (DMA)
-        run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
+        run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
       else
-        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
+        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
     } else if constexpr (MIXED) {
       if (tier == 1)
-        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
+        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
       else
-        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, sp, dyn_lds);
+        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
     }
-    if constexpr (PH == 1) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_active, &s_flag);
+    if constexpr (PH == 1) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_tiles, &s_flag);
   }
 }
 
@@ -1048,8 +1119,13 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   a.nbB = d.H / rows_b(nt);
   a.nsplit = 1;
   const int64_t max_active = (int64_t)(d.T * d.k < d.E ? d.T * d.k : d.E) + (d.Ep - d.E);
+  // Tiles: at most one per active expert plus one per further 16 rows.  The
+  // grid is sized for one tile per expert up to T = 16 (more tiles there
+  // need repeated ids; the work-groups then stride over the extra units).
+  const int64_t max_tiles = d.T <= 16 ? max_active : max_active + ((int64_t)d.T * d.kp + 15) / 16;
   for (int ph = 0; ph < 2; ++ph) {
-    const size_t lds = (size_t)DW * WAVE_LDS;  // per-wave weight slices / partial tiles
+    // per-wave weight slices / partial tiles, then the per-expert row counts
+    const size_t lds = (size_t)DW * WAVE_LDS + (((size_t)(d.Ep + 1) / 2 * 4 + 15) & ~(size_t)15);
     if (ph == 1) {
       // Few down units (large experts, few active): split each (expert, row
       // block) contraction over up to kDecodeMaxSplit work-groups, each with
@@ -1058,7 +1134,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
       const int st = resident_work_groups(
           reinterpret_cast<const void*>(pick_kernel(d.bf, 1, mixed, false)), DNT, lds, &resident);
       if (st) return st;
-      const int64_t u1 = max_active * a.nbB;
+      const int64_t u1 = max_tiles * a.nbB;
       int64_t sp = u1 > 0 ? resident / u1 : 1;
       const int64_t cap = (d.I / 128) / 4;
       if (sp > cap) sp = cap;
@@ -1074,7 +1150,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     // the wave's k-range fits its weight region and the unit's scales its scale area
     const bool dma = (nkb_split + 3) / 4 <= WAVE_W / (rs * 1024) && rs * 16 * ng * 2 <= WAVE_S;
     const decode_kernel_t kern = pick_kernel(d.bf, ph, mixed, dma);
-    const int64_t units = max_active * (ph == 0 ? a.nbA : (int64_t)a.nbB * a.nsplit);
+    const int64_t units = max_tiles * (ph == 0 ? a.nbA : (int64_t)a.nbB * a.nsplit);
     int resident = 0;
     const int st0 = resident_work_groups(reinterpret_cast<const void*>(kern), DNT, lds, &resident);
     if (st0) return st0;
