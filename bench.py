@@ -428,6 +428,17 @@ def measure_configs(dev, reps):
     rows += prefill_rows([_prefill_call(dev, "mixtral", layers[0])], max(3, reps // 10))
     del layers
     torch.cuda.empty_cache()
+
+    # Router (fp32 softmax -> top-k -> renormalise) on the seeded logits of
+    # Qwen3 (128 experts, top-8) at decode and prefill batch sizes.
+    from exq_amd.kernels import fused_topk
+    cfg = synth.CONFIGS["qwen3"]
+    for T in (16, 2048):
+        lg = torch.from_numpy(synth.router_logits(cfg, T, synth.seed_for(cfg) + 7)).to(dev)
+        ms = _graph_time(lambda lg=lg: fused_topk(lg, cfg.top_k, cfg.renormalize), reps)
+        rows.append({"config": "router_qwen3", "batch": T, "experts": cfg.n_experts,
+                     "top_k": cfg.top_k, "us_per_call": round(ms * 1e3, 2)})
+        log(f"config router qwen3 T={T}: {ms * 1e3:.2f} us")
     return rows
 
 

@@ -52,6 +52,7 @@ _SIGNATURES = {
     "exq_last_error": ([], C.c_char_p),
     "exq_status_name": ([_INT], C.c_char_p),
     "exq_moe_align_block_size": ([_P, _INT, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _INT, _P], _INT),
+    "exq_topk_softmax": ([_P, _INT, _I64, _I64, _I64, _INT, _P, _INT, _P, _INT, _P], _INT),
     "exq_build_ends_from_slots": ([_P, _I64, _P, _I64, _I64, _P, _P, _P], _INT),
     "exq_dispatch": ([_P, _INT, _I64, _I64, _P, _P, _P, _P], _INT),
     "exq_gather_hidden": ([_P, _INT, _I64, _I64, _P, _I64, _I64, _P, _P], _INT),

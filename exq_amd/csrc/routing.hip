@@ -400,6 +400,76 @@ int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, 
   return check_launch("tg_from_ends_kernel");
 }
 
+// ---------------------------------------------------------------------------
+// Router: fp32 softmax over a token's expert logits, the top-k experts, and
+// optionally their weights renormalised to sum to one.  One wave per token;
+// lane l holds logits l, l + 64, ...  Softmax is monotonic, so the top-k is
+// taken on the logits themselves (largest first, equal logits to the lower
+// expert id): the ids never depend on how exp() rounds.  The denominator is
+// a fixed-order wave reduction (deterministic).
+template <int MAXC>  // logits per lane: E <= 64 * MAXC
+__global__ void __launch_bounds__(256) topk_softmax_kernel(const void* logits, int ldt, int T,
+                                                          int E, int k, int renorm, void* ids,
+                                                          int idt, void* wts, int wdt) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= T) return;  // (wave-uniform)
+  float v[MAXC];
+  float m = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    const int e = lane + 64 * c;
+    v[c] = e < E ? load_as_f32(logits, ldt, (int64_t)row * E + e) : -INFINITY;
+    m = fmaxf(m, v[c]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  float sum = 0.f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c)
+    if (lane + 64 * c < E) sum += expf(v[c] - m);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+  const float inv = 1.0f / sum;
+  uint32_t taken = 0u;  // bit c: logit c of this lane already chosen
+  float mine = 0.f;     // lane j < k: weight of the j-th choice
+  for (int j = 0; j < k; ++j) {
+    float bv = -INFINITY;
+    int be = INT32_MAX;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const int e = lane + 64 * c;
+      if (e < E && !((taken >> c) & 1u) && (v[c] > bv || be == INT32_MAX)) {
+        bv = v[c];
+        be = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {  // larger logit, then lower id
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    if ((be & 63) == lane) taken |= 1u << (be >> 6);
+    if (lane == j) mine = expf(bv - m) * inv;
+    if (lane == 0) {
+      if (idt == EXQ_DTYPE_I64)
+        reinterpret_cast<int64_t*>(ids)[(int64_t)row * k + j] = be;
+      else
+        reinterpret_cast<int32_t*>(ids)[(int64_t)row * k + j] = be;
+    }
+  }
+  if (renorm) {  // sum of the k weights in choice order
+    float ws = 0.f;
+    for (int j = 0; j < k; ++j) ws += __shfl(mine, j, 64);
+    mine = mine / ws;
+  }
+  if (lane < k) store_from_f32(wts, wdt, (int64_t)row * k + lane, mine);
+}
+
 }  // namespace exq
 
 using namespace exq;
@@ -465,4 +535,35 @@ extern "C" int exq_moe_align_block_size(const void* topk_ids, int ids_dtype, int
                      (int)sorted_capacity, expert_ids, (int)expert_ids_capacity,
                      num_tokens_post_pad, cumsum, pad_sorted_token_ids ? 1 : 0);
   return check_launch("align_kernel");
+}
+
+extern "C" int exq_topk_softmax(const void* logits, int logits_dtype, int64_t n_tokens,
+                                int64_t n_experts, int64_t top_k, int renormalize,
+                                void* topk_ids, int ids_dtype, void* topk_weights,
+                                int weights_dtype, exq_stream stream) {
+  EXQ_REQUIRE(logits_dtype == EXQ_DTYPE_F32 || is_act_dtype(logits_dtype),
+              "exq_topk_softmax: logits dtype must be f32, f16 or bf16");
+  EXQ_REQUIRE(is_index_dtype(ids_dtype), "exq_topk_softmax: ids dtype must be i32 or i64");
+  EXQ_REQUIRE(weights_dtype == EXQ_DTYPE_F32 || is_act_dtype(weights_dtype),
+              "exq_topk_softmax: weights dtype must be f32, f16 or bf16");
+  EXQ_REQUIRE(n_tokens >= 0 && n_tokens <= INT32_MAX / 4,
+              "exq_topk_softmax: n_tokens=%lld out of range", (long long)n_tokens);
+  EXQ_REQUIRE(n_experts >= 1 && n_experts <= 1024,
+              "exq_topk_softmax: n_experts=%lld must be in [1, 1024]", (long long)n_experts);
+  EXQ_REQUIRE(top_k >= 1 && top_k <= n_experts && top_k <= 64,
+              "exq_topk_softmax: top_k=%lld must be in [1, min(n_experts, 64)]",
+              (long long)top_k);
+  if (n_tokens == 0) return EXQ_SUCCESS;
+  EXQ_REQUIRE(logits && topk_ids && topk_weights, "exq_topk_softmax: null pointer");
+  const dim3 g((unsigned)((n_tokens + 3) / 4));
+  const hipStream_t s = as_stream(stream);
+  if (n_experts <= 256)
+    hipLaunchKernelGGL(topk_softmax_kernel<4>, g, dim3(256), 0, s, logits, logits_dtype,
+                       (int)n_tokens, (int)n_experts, (int)top_k, renormalize ? 1 : 0, topk_ids,
+                       ids_dtype, topk_weights, weights_dtype);
+  else
+    hipLaunchKernelGGL(topk_softmax_kernel<16>, g, dim3(256), 0, s, logits, logits_dtype,
+                       (int)n_tokens, (int)n_experts, (int)top_k, renormalize ? 1 : 0, topk_ids,
+                       ids_dtype, topk_weights, weights_dtype);
+  return check_launch("topk_softmax_kernel");
 }

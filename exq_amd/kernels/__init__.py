@@ -10,6 +10,7 @@ from .moe_grouped_gemm import moe_grouped_gemm, sort_tokens_by_expert, unsort_ou
 from .moe_int4_kernel import (moe_int4_forward, moe_int4_full_forward, pack_experts_int4,
                               pack_int4_weights)
 from . import exq_dispatch
+from .exq_dispatch import fused_topk
 
 __all__ = [
     "moe_grouped_gemm",
@@ -26,4 +27,5 @@ __all__ = [
     "MixedExpertBank",
     "quantize_int8_rows",
     "exq_dispatch",
+    "fused_topk",
 ]

@@ -138,3 +138,36 @@ def silu_and_mul(input: torch.Tensor, out: torch.Tensor) -> None:
     _lib.check(L.exq_silu_and_mul(input.data_ptr(), _lib.dtype_code(input.dtype), rows,
                                   two_i // 2, out.data_ptr(), _lib.stream_handle(dev)),
                "silu_and_mul")
+
+
+def fused_topk(gating_output: torch.Tensor, topk: int, renormalize: bool,
+               ids_dtype: torch.dtype = torch.int32,
+               weights_dtype: torch.dtype = torch.float32):
+    """Router on the GPU: fp32 softmax over ``gating_output`` [T, E], the top-k
+    experts per token (descending, equal logits to the lower id) and their
+    softmax weights, divided by their sum when ``renormalize``.
+
+    Returns ``(topk_weights [T, k], topk_ids [T, k])`` like SGLang's
+    ``fused_topk``; the reference computes the same routing with
+    ``F.softmax`` + ``torch.topk`` + a division by the sum
+    (exq/codegen/triton_emitter.py:273-277) and its SGLang hook consumes it as
+    ``dispatch_output.topk_output`` (exq/runtime/sglang_backend.py:88-90).
+    """
+    if gating_output.dim() != 2:
+        raise ValueError("gating_output must be [T, E]")
+    g = gating_output if gating_output.is_contiguous() else gating_output.contiguous()
+    dev = _lib.require_gpu(g)
+    T, E = g.shape
+    if not 1 <= topk <= min(E, 64):
+        raise ValueError(f"topk={topk} must be in [1, min(E, 64)]")
+    if E > 1024:
+        raise ValueError(f"E={E} > 1024 experts is not supported")
+    ids = torch.empty(T, topk, dtype=ids_dtype, device=dev)
+    wts = torch.empty(T, topk, dtype=weights_dtype, device=dev)
+    L = _lib.lib()
+    _lib.check(L.exq_topk_softmax(g.data_ptr(), _lib.dtype_code(g.dtype), T, E, topk,
+                                  1 if renormalize else 0, ids.data_ptr(),
+                                  _lib.dtype_code(ids.dtype), wts.data_ptr(),
+                                  _lib.dtype_code(wts.dtype), _lib.stream_handle(dev)),
+               "fused_topk")
+    return wts, ids

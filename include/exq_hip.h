@@ -66,6 +66,20 @@ const char* exq_status_name(int status);
 /* ---- routing preparation ------------------------------------------------ */
 
 /*
+ * Router: logits [T, E] (f32 | f16 | bf16) -> topk_ids [T, k] (i32 | i64) and
+ * topk_weights [T, k] (f32 | f16 | bf16).  Replaces the routing the reference
+ * runs before dispatch (exq/codegen/triton_emitter.py:273-277: F.softmax over
+ * the router logits, torch.topk, weights divided by their sum), whose output
+ * the SGLang hook receives as dispatch_output.topk_output
+ * (exq/runtime/sglang_backend.py:88-90).  Softmax in fp32; experts in
+ * descending order, equal logits to the lower id; renormalize != 0 divides
+ * the k weights by their sum.  E <= 1024, 1 <= k <= min(E, 64).
+ */
+int exq_topk_softmax(const void* logits, int logits_dtype, int64_t n_tokens,
+                     int64_t n_experts, int64_t top_k, int renormalize, void* topk_ids,
+                     int ids_dtype, void* topk_weights, int weights_dtype, exq_stream stream);
+
+/*
  * Block-padded expert layout.  Replaces sgl_kernel.moe_align_block_size as
  * called at exq/runtime/sglang_backend.py:102-109 (num_experts = E + 1,
  * block_size = 16).  Bucket b = id + 1 (bucket 0 collects id == -1);
