@@ -26,6 +26,7 @@ import torch
 from ..kernels.exq_artifact import PRECISION_TO_INT
 from ..kernels.fused_moe import MixedExpertBank, fused_experts, fused_experts_mixed
 from ..kernels.moe_int4_kernel import pack_experts_int4
+from .pack_cache import PackedWeightCache
 
 logger = logging.getLogger(__name__)
 
@@ -63,8 +64,12 @@ def _get_or_pack(layer, backend: "ExQSGLangBackend | None" = None) -> dict:
             tiers = None
     cache = {"n_experts": E, "inter2": w13.shape[1], "hidden": w13.shape[2]}
     if tiers is None:
-        cache["w1_packed"], cache["w1_scales"] = pack_experts_int4(w13.to(torch.float16), 128)
-        cache["w2_packed"], cache["w2_scales"] = pack_experts_int4(w2.to(torch.float16), 128)
+        if backend is not None and backend.disk_cache is not None and layer_id is not None:
+            (cache["w1_packed"], cache["w1_scales"], cache["w2_packed"],
+             cache["w2_scales"]) = backend.disk_cache.get_or_pack(f"layer{layer_id}", w13, w2)
+        else:
+            cache["w1_packed"], cache["w1_scales"] = pack_experts_int4(w13.to(torch.float16), 128)
+            cache["w2_packed"], cache["w2_scales"] = pack_experts_int4(w2.to(torch.float16), 128)
         cache["bank"] = None
     else:
         act = w13.dtype if w13.dtype in (torch.float16, torch.bfloat16) else torch.bfloat16
@@ -106,7 +111,8 @@ def _exq_forward_cuda(self_method, layer, dispatch_output, _original_forward_cud
 class ExQSGLangBackend:
     """Holds the artifact's plan and the per-layer weight cache."""
 
-    def __init__(self, artifact_path: str, honor_plan: bool = True):
+    def __init__(self, artifact_path: str, honor_plan: bool = True,
+                 pack_cache_dir: str | None = None):
         with open(artifact_path, encoding="utf-8") as f:
             artifact = json.load(f)
         qa = artifact.get("quant_assignments") or artifact.get("quant_plan") or {}
@@ -117,6 +123,8 @@ class ExQSGLangBackend:
         self.n_layers = max(self.assignments) + 1 if self.assignments else 0
         self.artifact_path = artifact_path
         self.honor_plan = honor_plan
+        # INT4 layers packed once and kept on disk across runs (None: in memory only)
+        self.disk_cache = PackedWeightCache(pack_cache_dir) if pack_cache_dir else None
         logger.info("ExQ SGLang backend: %d layers (%d assignments)", self.n_layers, len(qa))
 
     def clear_cache(self) -> None:
@@ -126,18 +134,26 @@ class ExQSGLangBackend:
     def cache_stats(self) -> dict:
         with _cache_lock:
             n = len(_exq_packed_cache)
-        return {"n_layers_cached": n, "n_layers_in_artifact": self.n_layers}
+        st = {"n_layers_cached": n, "n_layers_in_artifact": self.n_layers}
+        if self.disk_cache is not None:
+            st.update(disk_hits=self.disk_cache.hits, disk_misses=self.disk_cache.misses)
+        return st
 
 
-def patch_sglang(artifact_path: str, honor_plan: bool = True) -> ExQSGLangBackend:
-    """Replace UnquantizedFusedMoEMethod.forward_cuda for the artifact's layers."""
+def patch_sglang(artifact_path: str, honor_plan: bool = True,
+                 pack_cache_dir: str | None = None) -> ExQSGLangBackend:
+    """Replace UnquantizedFusedMoEMethod.forward_cuda for the artifact's layers.
+
+    ``pack_cache_dir``: keep the packed INT4 banks on disk there (one
+    safetensors file per layer), so later runs load instead of repacking."""
     global _original_forward
     try:
         from sglang.srt.layers.quantization.unquant import UnquantizedFusedMoEMethod
     except ImportError as exc:
         raise ImportError("SGLang not installed: pip install sglang") from exc
 
-    backend = ExQSGLangBackend(artifact_path, honor_plan=honor_plan)
+    backend = ExQSGLangBackend(artifact_path, honor_plan=honor_plan,
+                               pack_cache_dir=pack_cache_dir)
     if getattr(UnquantizedFusedMoEMethod, "_exq_patched", False):
         logger.warning("ExQ: re-patching SGLang (cache cleared)")
         backend.clear_cache()
