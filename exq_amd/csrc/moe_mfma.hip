@@ -627,8 +627,16 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     g.inter = I;
     g.skip_i4 = tile ? 1 : 0;
     g.skip_bf = tile_bf ? 1 : 0;
-    // Without a tier array every expert is INT4: the tiled kernel does it all.
-    const bool old_kernel = !tile || tier != nullptr;
+    // The grouped kernel runs only for what the tiles leave: INT8 experts, and
+    // INT4 / BF16 experts whose tiled kernel does not apply.  Without a tier
+    // array every expert is INT4.  A tile kernel runs only if its tier has
+    // experts (an empty launch still costs its grid).
+    const bool has_i4 = tier == nullptr || b13.i4 != nullptr;
+    const bool has_bf = tier != nullptr && b13.bf16 != nullptr;
+    const bool old_kernel = tier == nullptr ? !tile
+                                            : (b13.i8 != nullptr || (has_i4 && !tile) ||
+                                               (has_bf && !tile_bf));
+    const bool run_tile = tile && has_i4, run_tile_bf = tile_bf && has_bf;
     float* rs = reinterpret_cast<float*>(ws + L.rs);
     // gate/up + SiLU: x = hidden, K = H, rows = 2I, out = mid [n, I] (sorted rows)
     g.n_blocks = I / 16;
@@ -643,11 +651,11 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
-    if (tile_bf) {
+    if (run_tile_bf) {
       st = launch_tile_gemm(0, MODE_GATEUP, bf, g, nullptr, 0, (int64_t)T * H * 2, L.tg_cap, s);
       if (st) return st;
     }
-    if (tile) {
+    if (run_tile) {
       st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
       if (st) return st;
       st = launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s);
@@ -669,11 +677,11 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
-    if (tile_bf) {
+    if (run_tile_bf) {
       st = launch_tile_gemm(0, MODE_DOWN, bf, g, nullptr, 0, 0, L.tg_cap, s);
       if (st) return st;
     }
-    if (tile) {
+    if (run_tile) {
       st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
       if (st) return st;
       st = launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s);
