@@ -781,6 +781,133 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
   }
 }
 
+// INT4 gate/up unit whose k-range is longer than the wave's LDS region
+// holds (large hidden sizes): the range is copied and consumed in chunks of
+// CK k-blocks, each a whole-slice LDS DMA like run_unit_dma's, accumulating
+// in registers across chunks.  A wave's region is its own, so a chunk's copy
+// only waits for the wave's own reads of the previous chunk.  Twice the bytes
+// of the register ring are in flight per wave (8 KiB, 32 rows x 4 k-blocks).
+// The group scales of the whole k-range are copied once with 4-byte LDS DMA
+// (row r's groups g_lo.. as nd dwords from its aligned start).
+template <bool BF, int NT>
+__device__ __forceinline__ void run_unit_dma_chunked(const LayerArgs& a, const Route& rt, int e,
+                                                     int blk, int tile, unsigned char* lds) {
+  constexpr int PH = 0;
+  using G = Geo<2, PH, NT>;
+  constexpr int RS = G::RS, CK = G::CK;
+  constexpr int DA = NT == 4 ? 1 : 2;  // activation k-blocks in flight
+  const UnitCtx<2, PH, NT> u(a, e, blk, 0);
+  unsigned char* region = lds + u.wave * WAVE_LDS;
+
+  const int g_lo = u.lo >> a.gshift;
+  const int ngw = u.nmy > 0 ? ((u.lo + u.nmy - 1) >> a.gshift) - g_lo + 1 : 1;
+  const int nd = (ngw * 2 + 2 + 3) >> 2;  // dwords per row (2 bytes of alignment slack)
+  {
+    unsigned char* dst = region + WAVE_W;
+    const int nflat = RS * 16 * nd;
+    for (int i0 = 0; i0 < nflat; i0 += 64) {  // wave-uniform trip count
+      const int f = i0 + u.lane;
+      const int rr = f / nd, d = f - (f / nd) * nd;
+      const bool in = f < nflat;
+      const int b0 = (u.row(a, blk, in ? rr : 0) * u.ng + g_lo) * 2;
+      dma4(in ? u.sr : u.snull, dst + i0 * 4, in ? (b0 & ~3) + d * 4 : 0);
+    }
+  }
+  const uint16_t* sc_lds = reinterpret_cast<const uint16_t*>(region + WAVE_W);
+  auto scale_at = [&](int rs, int kb) {
+    const int row = u.row(a, blk, rs * 16 + u.r16);
+    const int e0 = ((row * u.ng + g_lo) * 2) & 2;
+    return f16_bits_to_f32(sc_lds[((rs * 16 + u.r16) * nd * 4 + e0) / 2 + ((kb >> a.gshift) - g_lo)]);
+  };
+
+  const int r_begin = tile * NT * 16;
+  int sl[NT];
+  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, r_begin, sl));
+  const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(dq_magic));
+
+  for (int r0 = r_begin; r0 < cnt && r0 < r_begin + NT * 16; r0 += NT * 16) {
+    const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
+    const int ntiles = (cc + 15) >> 4;
+    int xo[NT];
+#pragma unroll
+    for (int tt = 0; tt < NT; ++tt) xo[tt] = u.xoff(a, sl[tt]);
+    f32x4_t tot[RS][NT];
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) tot[rs][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int c0 = 0; c0 < u.nmy; c0 += CK) {  // wave-uniform
+      const int nc = u.nmy - c0 < CK ? u.nmy - c0 : CK;
+      const int p4 = 4 * nc;               // 16-byte pieces per row in LDS
+      const int xm = (nc & 1) ? 3 : 7;     // swizzle mask keeps c ^ (rr & xm) < p4
+      if (c0 > 0) wave_lds_fence();        // this wave's reads of the last chunk are done
+      for (int j = 0; j < RS * nc; ++j) {  // 64 pieces per instruction
+        const int p = j * 64 + u.lane;
+        const int rr = p / p4;
+        const int c = (p - rr * p4) ^ (rr & xm);
+        dma16(u.wr, region + j * 1024, u.row(a, blk, rr) * u.rowbytes + (u.lo + c0) * 64 + c * 16);
+      }
+      uint4 areg[DA][4 * NT];
+      auto load_a = [&](int p, int kbl) {  // zeros past the chunk
+        const bool ok = kbl < nc;
+        const int kb = ok ? u.lo + c0 + kbl : u.lo;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt)
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            areg[p][tt * 4 + d] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(ok ? u.xr : u.xnull,
+                                                             xo[tt] + d * 16, kb * 256, 0));
+      };
+#pragma unroll
+      for (int p = 0; p < DA; ++p) load_a(p, p);
+      wait_vm_all();  // the chunk (and, the first time, the scales) has landed
+#pragma unroll
+      for (int kbl = 0; kbl < CK; ++kbl) {
+        const int p = kbl % DA;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+          if (tt < ntiles) {
+            uint4 xa[4];
+            f32x4_t init;
+            make_a<2, BF, PH>(&areg[p][tt * 4], xa, init);
+#pragma unroll
+            for (int rs = 0; rs < RS; ++rs) {
+              const int rr = rs * 16 + u.r16;
+              const int cpos = kbl * 4 + u.kq;
+              const int off = kbl < nc ? (rr * p4 + (cpos ^ (rr & xm))) * 16 : 0;
+              const uint4 w = *reinterpret_cast<const uint4*>(region + off);
+              f32x4_t acc = dmfma<BF>(xa[0], ddeq4(w.x, dq_mask, dq_magic), init);
+              acc = dmfma<BF>(xa[1], ddeq4(w.y, dq_mask, dq_magic), acc);
+              acc = dmfma<BF>(xa[2], ddeq4(w.z, dq_mask, dq_magic), acc);
+              acc = dmfma<BF>(xa[3], ddeq4(w.w, dq_mask, dq_magic), acc);
+              // past the chunk the activations (and so acc) are zero
+              const float sc = kbl < nc ? scale_at(rs, u.lo + c0 + kbl) : 0.f;
+              tot[rs][tt] += sc * acc;
+            }
+          }
+        }
+        if (kbl + DA < CK) load_a(p, kbl + DA);
+      }
+    }
+    wave_lds_fence();  // the last chunk's reads are done before the partial tiles
+    float4* red = reinterpret_cast<float4*>(region);
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs)
+#pragma unroll
+      for (int tt = 0; tt < NT; ++tt)
+        if (tt < ntiles)
+          red[(rs * NT + tt) * 64 + u.lane] =
+              float4{tot[rs][tt][0], tot[rs][tt][1], tot[rs][tt][2], tot[rs][tt][3]};
+    __syncthreads();
+    finish_pass<2, BF, PH, NT>(a, u, lds, sl, cc, ntiles, blk);
+    __syncthreads();  // LDS regions free again
+  }
+}
+
 // General unit (any tier, any K): each wave streams k-blocks lo .. lo+nmy-1
 // through a register ring of P k-blocks.  Every ring slot is refilled
 // unconditionally: a k-block beyond the wave's range is read through a
@@ -972,7 +1099,7 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
 // unit u is row block u % nb of the (u / nb)-th active expert).
 // Four waves per SIMD (four work-groups per CU, at most 128 VGPRs) except
 // the mixed-tier down kernel, whose register use needs two.
-template <bool BF, int PH, int NT, bool MIXED, bool DMA>
+template <bool BF, int PH, int NT, bool MIXED, int PATH>  // INT4 path: 0 ring, 1 LDS, 2 chunked LDS
 __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_kernel(LayerArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
   __shared__ Route rt;
@@ -1018,8 +1145,10 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
     const int e = t == 0 ? select_expert(ai, word, incl, c) : select_tiled_expert(a, cntw, rt, t, ai);
     const int tier = MIXED ? __builtin_amdgcn_readfirstlane((int)a.tier[e]) : 2;
     if (!MIXED || tier == 2) {
-      if constexpr (DMA)
+      if constexpr (PATH == 1)
         run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
+      else if constexpr (PATH == 2 && PH == 0)
+        run_unit_dma_chunked<BF, NT>(a, rt, e, blk, t, dyn_lds);
       else
         run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
     } else if constexpr (MIXED) {
@@ -1035,18 +1164,19 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
 typedef void (*decode_kernel_t)(LayerArgs);
 
 template <bool BF, int PH>
-decode_kernel_t pick_ph(bool mixed, bool dma) {
-  if (mixed) return dma ? moe_decode_kernel<BF, PH, 1, true, true> : moe_decode_kernel<BF, PH, 1, true, false>;
-  return dma ? moe_decode_kernel<BF, PH, 1, false, true> : moe_decode_kernel<BF, PH, 1, false, false>;
+decode_kernel_t pick_ph(bool mixed, int path) {
+  if (mixed) return path == 1 ? moe_decode_kernel<BF, PH, 1, true, 1> : moe_decode_kernel<BF, PH, 1, true, 0>;
+  if (PH == 0 && path == 2) return moe_decode_kernel<BF, 0, 1, false, 2>;
+  return path == 1 ? moe_decode_kernel<BF, PH, 1, false, 1> : moe_decode_kernel<BF, PH, 1, false, 0>;
 }
 
 // One 16-row tile per pass: units with more rows take further passes (each
 // re-reads its weight slice, from L2), which measured faster at T = 32 and 64
 // than kernels holding two or four tiles per pass (higher register use, lower
 // occupancy).
-decode_kernel_t pick_kernel(bool bf, int ph, bool mixed, bool dma) {
-  if (bf) return ph == 0 ? pick_ph<true, 0>(mixed, dma) : pick_ph<true, 1>(mixed, dma);
-  return ph == 0 ? pick_ph<false, 0>(mixed, dma) : pick_ph<false, 1>(mixed, dma);
+decode_kernel_t pick_kernel(bool bf, int ph, bool mixed, int path) {
+  if (bf) return ph == 0 ? pick_ph<true, 0>(mixed, path) : pick_ph<true, 1>(mixed, path);
+  return ph == 0 ? pick_ph<false, 0>(mixed, path) : pick_ph<false, 1>(mixed, path);
 }
 
 }  // namespace
@@ -1132,7 +1262,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
       // at least four k-blocks, to fill the resident round.
       int resident = 0;
       const int st = resident_work_groups(
-          reinterpret_cast<const void*>(pick_kernel(d.bf, 1, mixed, false)), DNT, lds, &resident);
+          reinterpret_cast<const void*>(pick_kernel(d.bf, 1, mixed, 0)), DNT, lds, &resident);
       if (st) return st;
       const int64_t u1 = max_tiles * a.nbB;
       int64_t sp = u1 > 0 ? resident / u1 : 1;
@@ -1149,7 +1279,16 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     const int ng = nkb >> a.gshift;             // the unit's whole scale rows are copied
     // the wave's k-range fits its weight region and the unit's scales its scale area
     const bool dma = (nkb_split + 3) / 4 <= WAVE_W / (rs * 1024) && rs * 16 * ng * 2 <= WAVE_S;
-    const decode_kernel_t kern = pick_kernel(d.bf, ph, mixed, dma);
+    // Gate/up with a longer k-range (all INT4): chunked LDS copies, when the
+    // k-range's scale dwords (rows x nd, whole 256-byte DMA steps) fit the
+    // scale area.
+    bool chunked = false;
+    if (ph == 0 && !mixed && !dma) {
+      const int gkb = 1 << a.gshift, span = (nkb_split + 3) / 4;
+      const int ngw = (span + gkb - 1) / gkb + 1, nd = (ngw * 2 + 2 + 3) / 4;
+      chunked = ((rs * 16 * nd + 63) / 64) * 256 <= WAVE_S;
+    }
+    const decode_kernel_t kern = pick_kernel(d.bf, ph, mixed, dma ? 1 : (chunked ? 2 : 0));
     const int64_t units = max_tiles * (ph == 0 ? a.nbA : (int64_t)a.nbB * a.nsplit);
     int resident = 0;
     const int st0 = resident_work_groups(reinterpret_cast<const void*>(kern), DNT, lds, &resident);

@@ -187,6 +187,26 @@ def test_fused_down_split_contraction(name, H, I, E, k, T, device):
             assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid), out)
 
 
+@pytest.mark.parametrize("H,I,gs", [(4096, 256, 128), (2560, 256, 128), (4096, 256, 256)])
+@pytest.mark.parametrize("T", [1, 5, 40])
+def test_fused_chunked_gateup(H, I, gs, T, device):
+    """Hidden sizes past 2048 give each wave more k-blocks than its LDS region
+    holds: the gate/up unit copies its slice in chunks (4096: two full
+    chunks; 2560: 4 + 1 k-blocks; group size 256 shares a scale between
+    k-blocks)."""
+    from exq_amd.kernels import fused_experts, pack_experts_int4
+    cfg = synth.MoeConfig(f"chunk_{H}", 33, H, I, 4, 2, True, zipf=False)
+    banner(f"fused chunked H={H} gs={gs} T={T}")
+    w13, w2 = synth.expert_weights_gpu(4, I, H, 700 + H, device)
+    p13, s13 = pack_experts_int4(w13, group_size=gs)
+    p2, s2 = pack_experts_int4(w2, group_size=gs)
+    ids, w, tid, tw = _routing(cfg, T, device)
+    x = _hidden(T, H, 9 + T, device)
+    out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, f"chunked H={H} gs={gs} T={T}")
+
+
 def test_moe_int4_forward_sorted_output(device):
     from exq_amd.kernels import moe_int4_forward, sort_tokens_by_expert
     from oracle import moe
