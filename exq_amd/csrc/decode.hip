@@ -508,7 +508,7 @@ __device__ __forceinline__ void make_a(const uint4* raw, uint4 (&xa)[4], f32x4_t
 // After a pass's k-loop: the four waves' partial tiles sit in their LDS
 // regions; sum them and write `mid` (gate/up: SiLU(gate) * up) or the fp32
 // partial rows (down).
-template <int TIER, bool BF, int PH, int NT>
+template <int TIER, bool BF, int PH, int NT, int WSTRIDE = WAVE_LDS>  // wave w's tiles at lds + w*WSTRIDE
 __device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TIER, PH, NT>& u,
                                             const unsigned char* lds, const int (&sl)[NT], int cc,
                                             int ntiles, int blk) {
@@ -523,7 +523,7 @@ __device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TI
   using G = Geo<TIER, PH, NT>;
   constexpr int RS = G::RS, ROWS_B = G::ROWS_B;
   auto red = [&](int w, int rs, int tt) {
-    return reinterpret_cast<const float4*>(lds + w * WAVE_LDS)[(rs * NT + tt) * 64 + u.lane];
+    return reinterpret_cast<const float4*>(lds + w * WSTRIDE)[(rs * NT + tt) * 64 + u.lane];
   };
   // lane (r16, kq) of tile tt holds rows tt*16 + 4*kq + i, column r16
   if constexpr (PH == 0) {
@@ -779,6 +779,130 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
     finish_pass<2, BF, PH, NT>(a, u, lds, sl, cc, ntiles, blk);
     __syncthreads();  // LDS regions free again
   }
+}
+
+// LDS-path unit with the slice copied k-block by k-block into separate LDS
+// arrays (one per k-block position, all four waves' copies), so that the
+// k-loop starts on k-block 0 while later k-blocks are still landing: the
+// copies go out in the order scales, k-block 0, activations 0-1, k-blocks
+// 1.., and each k-block waits only for the loads issued up to it.  A wave
+// always issues CK k-block copies (through an empty buffer past its range),
+// so those waits are fixed counts.  Separate arrays let the compiler see
+// that reading one k-block cannot touch another's pending copy.  The partial
+// tiles go to k-block 0's array once the loop is done.
+template <bool BF, int PH>
+__device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Route& rt, int e, int blk,
+                                            int sp, int tile) {
+  constexpr int NT = 1;
+  using G = Geo<2, PH, NT>;
+  constexpr int RS = G::RS, CK = G::CK;
+  static_assert(CK == 2 || CK == 4, "k-block arrays");
+  constexpr int KBB = RS * 1024;  // one k-block of the wave's rows
+  __shared__ __attribute__((aligned(16))) unsigned char s_kb0[DW * KBB];
+  __shared__ __attribute__((aligned(16))) unsigned char s_kb1[DW * KBB];
+  __shared__ __attribute__((aligned(16))) unsigned char s_kb2[CK > 2 ? DW * KBB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char s_kb3[CK > 2 ? DW * KBB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char s_sc[DW * WAVE_S];
+  const UnitCtx<2, PH, NT> u(a, e, blk, sp);
+  auto kbuf = [&](int kbl) {
+    return (kbl == 0 ? s_kb0 : kbl == 1 ? s_kb1 : kbl == 2 ? s_kb2 : s_kb3) + u.wave * KBB;
+  };
+  // k-block kbl of the wave's range: RS instructions of 16 rows x 4 pieces;
+  // LDS piece (row, c') holds source piece c' ^ (row & 3)
+  const int dr = u.lane >> 2, dc = (u.lane & 3) ^ (dr & 3);
+  auto copy_kb = [&](int kbl) {
+    const bool ok = kbl < u.nmy;
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs)
+      dma16(ok ? u.wr : u.wnull, kbuf(kbl) + rs * 1024,
+            ok ? u.row(a, blk, rs * 16 + dr) * u.rowbytes + (u.lo + kbl) * 64 + dc * 16 : 0);
+  };
+  unsigned char* scl = s_sc + u.wave * WAVE_S;
+  {  // the unit's scale block (as run_unit_dma)
+    const int blk_bytes = 16 * u.ng * 2;
+    int goff;
+    if constexpr (PH == 0) {
+      const int half = u.lane * 16 < blk_bytes ? 0 : 1;
+      goff = (half ? a.I + blk * 16 : blk * 16) * u.ng * 2 + u.lane * 16 - half * blk_bytes;
+    } else {
+      goff = blk * G::ROWS_B * u.ng * 2 + u.lane * 16;
+    }
+    const bool in = u.lane * 16 < RS * blk_bytes;
+    dma16(in ? u.sr : u.snull, scl, in ? goff : 0);
+  }
+  copy_kb(0);
+  const int r_begin = tile * 16;
+  int sl[NT];
+  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, r_begin, sl));
+  const int xo = u.xoff(a, sl[0]);
+  uint4 areg[2][4];
+  auto load_a = [&](int p, int kbl) {  // zeros past the wave's range
+    const bool ok = kbl < u.nmy;
+    const int kb = ok ? u.lo + kbl : u.lo;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      areg[p][d] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(ok ? u.xr : u.xnull, xo + d * 16,
+                                                       kb * 256, 0));
+  };
+  load_a(0, 0);
+  load_a(1, 1);
+#pragma unroll
+  for (int kbl = 1; kbl < CK; ++kbl) copy_kb(kbl);
+
+  const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
+  asm volatile("" : "+v"(dq_magic));
+  const uint16_t* sc_lds = reinterpret_cast<const uint16_t*>(scl);
+  const int cc = cnt - r_begin < 16 ? cnt - r_begin : 16;
+  f32x4_t tot[RS];
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs) tot[rs] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Loads in flight behind k-block kbl's copy, in issue order: for kbl = 0
+  // the second activation fragments and copies 1..CK-1; for kbl >= 1 the
+  // later copies and the activation loads issued in the loop (k-blocks 2..,
+  // issued after every copy, so they never count as behind a copy).
+#pragma unroll
+  for (int kbl = 0; kbl < CK; ++kbl) {
+    const int p = kbl & 1;
+    if (kbl == 0) {
+      wait_vm_le<4 + (CK - 1) * RS>();
+    } else if (kbl == 1) {
+      wait_vm_le<(CK - 2) * RS + (CK > 2 ? 4 : 0)>();  // + k-block 2's activations
+    } else if (kbl == 2) {
+      wait_vm_le<4>();  // k-block 3's activations
+    } else {
+      wait_vm_all();
+    }
+    uint4 xa[4];
+    f32x4_t init;
+    make_a<2, BF, PH>(areg[p], xa, init);
+    const unsigned char* kb_lds = kbuf(kbl);
+#pragma unroll
+    for (int rs = 0; rs < RS; ++rs) {
+      const uint4 w = *reinterpret_cast<const uint4*>(
+          kb_lds + rs * 1024 + (u.r16 * 4 + (u.kq ^ (u.r16 & 3))) * 16);
+      f32x4_t acc = dmfma<BF>(xa[0], ddeq4(w.x, dq_mask, dq_magic), init);
+      acc = dmfma<BF>(xa[1], ddeq4(w.y, dq_mask, dq_magic), acc);
+      acc = dmfma<BF>(xa[2], ddeq4(w.z, dq_mask, dq_magic), acc);
+      acc = dmfma<BF>(xa[3], ddeq4(w.w, dq_mask, dq_magic), acc);
+      // past the wave's range the activations (and so acc) are zero
+      const float sc =
+          kbl < u.nmy ? f16_bits_to_f32(sc_lds[(rs * 16 + u.r16) * u.ng + ((u.lo + kbl) >> a.gshift)])
+                      : 0.f;
+      tot[rs] += sc * acc;
+    }
+    if (kbl + 2 < CK) load_a(p, kbl + 2);
+  }
+  // partial tiles into k-block 0's array (this wave's reads of it are done)
+  wave_lds_fence();
+  float4* red = reinterpret_cast<float4*>(kbuf(0));
+#pragma unroll
+  for (int rs = 0; rs < RS; ++rs)
+    red[rs * 64 + u.lane] = float4{tot[rs][0], tot[rs][1], tot[rs][2], tot[rs][3]};
+  __syncthreads();
+  finish_pass<2, BF, PH, NT, KBB>(a, u, s_kb0, sl, cc, 1, blk);
+  __syncthreads();  // LDS arrays free again
 }
 
 // INT4 gate/up unit whose k-range is longer than the wave's LDS region
@@ -1104,7 +1228,10 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
   __shared__ Route rt;
   __shared__ int s_flag;
-  uint32_t* cntw = reinterpret_cast<uint32_t*>(dyn_lds + DW * WAVE_LDS);  // rows per expert
+  // rows per expert, behind the per-wave regions (the k-block LDS path keeps
+  // its slices in static arrays and has only this in dynamic LDS)
+  uint32_t* cntw =
+      reinterpret_cast<uint32_t*>(dyn_lds + (PATH == 1 && NT == 1 && !MIXED ? 0 : DW * WAVE_LDS));
   uint32_t word;
   int incl, c;
   const int n_active = route(a, rt, cntw, word, incl, c);
@@ -1145,7 +1272,9 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
     const int e = t == 0 ? select_expert(ai, word, incl, c) : select_tiled_expert(a, cntw, rt, t, ai);
     const int tier = MIXED ? __builtin_amdgcn_readfirstlane((int)a.tier[e]) : 2;
     if (!MIXED || tier == 2) {
-      if constexpr (PATH == 1)
+      if constexpr (PATH == 1 && NT == 1 && !MIXED)
+        run_unit_kb<BF, PH>(a, rt, e, blk, sp, t);
+      else if constexpr (PATH == 1)
         run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
       else if constexpr (PATH == 2 && PH == 0)
         run_unit_dma_chunked<BF, NT>(a, rt, e, blk, t, dyn_lds);
@@ -1289,16 +1418,18 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
       chunked = ((rs * 16 * nd + 63) / 64) * 256 <= WAVE_S;
     }
     const decode_kernel_t kern = pick_kernel(d.bf, ph, mixed, dma ? 1 : (chunked ? 2 : 0));
+    // (the all-INT4 LDS path keeps its slices in static arrays)
+    const size_t klds = dma && !mixed ? lds - (size_t)DW * WAVE_LDS : lds;
     const int64_t units = max_tiles * (ph == 0 ? a.nbA : (int64_t)a.nbB * a.nsplit);
     int resident = 0;
-    const int st0 = resident_work_groups(reinterpret_cast<const void*>(kern), DNT, lds, &resident);
+    const int st0 = resident_work_groups(reinterpret_cast<const void*>(kern), DNT, klds, &resident);
     if (st0) return st0;
     const int64_t grid = units < resident ? units : resident;
     const dim3 g((unsigned)(grid > 0 ? grid : 1));
     if (const hipEvent_t* ev = stage_events())  // start / stop of exactly this kernel
-      hipExtLaunchKernelGGL(kern, g, dim3(DNT), lds, s, ev[2 * ph], ev[2 * ph + 1], 0, a);
+      hipExtLaunchKernelGGL(kern, g, dim3(DNT), klds, s, ev[2 * ph], ev[2 * ph + 1], 0, a);
     else
-      hipLaunchKernelGGL(kern, g, dim3(DNT), lds, s, a);
+      hipLaunchKernelGGL(kern, g, dim3(DNT), klds, s, a);
     const int st = check_launch(ph == 0 ? "moe_decode_kernel<gate/up>" : "moe_decode_kernel<down>");
     if (st) return st;
   }
