@@ -239,6 +239,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
 }
 
+// A byte offset past every resource that a per-lane out-of-range access uses
+// (group scales of one expert, the partial rows; the host keeps both below
+// it): such a lane reads zero without a memory access, while the resource
+// itself stays wave-uniform.  (A per-lane choice of resource would make the
+// compiler loop over the distinct values, one load per iteration.)
+constexpr int OOB_OFF = 0x7ffffff0;
+
+// Wave-uniform copies of values the compiler cannot prove uniform, so that
+// buffer offsets and resource choices stay in scalar registers.
+__device__ __forceinline__ bool uni_b(bool v) { return __builtin_amdgcn_readfirstlane((int)v) != 0; }
+__device__ __forceinline__ int uni_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 
 // The batch's routed ids and active-expert bitmap, per work-group.
 struct Route {
@@ -451,7 +463,7 @@ struct UnitCtx {
     nmy = s0 + (((wave + 1) * (s1 - s0)) >> 2) - lo;  // k-blocks of this wave
     const Proj& W = PH == 0 ? a.w13 : a.w2;
     const int n_rows = PH == 0 ? 2 * a.I : a.H;
-    const int widx = a.index ? __builtin_amdgcn_readfirstlane(a.index[e]) : e;
+    const int widx = a.index ? uni_i(a.index[uni_i(e)]) : e;
     ebase = (int64_t)widx * n_rows;
     rowbytes = TIER == 2 ? K / 2 : (TIER == 1 ? K : 2 * K);
     const unsigned char* wbase =
@@ -595,7 +607,6 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
   // partial; a chunk of eight slots' loads is issued at once
   const int64_t set = (int64_t)a.T * a.kp * a.H;  // floats per partial set
   const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, a.nsplit * set * 4);
-  const __amdgpu_buffer_rsrc_t part_null = make_rsrc(a.part, 0);
   const int h0 = blk * ROWS_B;
   for (int idx = threadIdx.x; idx < a.T * (ROWS_B / 4); idx += DNT) {
     const int t = idx / (ROWS_B / 4);
@@ -616,14 +627,14 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
         wg[jj] = ok ? wgt : 0.f;
         pv[jj] = __builtin_bit_cast(
             float4, __builtin_amdgcn_raw_buffer_load_b128(
-                        ok ? part_r : part_null, ok ? ((t * a.kp + j) * a.H + h) * 4 : 0, 0,
+                        part_r, ok ? ((t * a.kp + j) * a.H + h) * 4 : OOB_OFF, 0,
                         CPOL_SC1));
         // further k-splits of the same row, in split order
         for (int sp = 1; sp < a.nsplit; ++sp) {
           const float4 q = __builtin_bit_cast(
               float4, __builtin_amdgcn_raw_buffer_load_b128(
-                          ok ? part_r : part_null,
-                          ok ? (int)((sp * set + (int64_t)(t * a.kp + j) * a.H + h) * 4) : 0, 0,
+                          part_r,
+                          ok ? (int)((sp * set + (int64_t)(t * a.kp + j) * a.H + h) * 4) : OOB_OFF, 0,
                           CPOL_SC1));
           pv[jj].x += q.x; pv[jj].y += q.y; pv[jj].z += q.z; pv[jj].w += q.w;
         }
@@ -700,7 +711,7 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
       goff = blk * G::ROWS_B * u.ng * 2 + u.lane * 16;
     }
     const bool in = u.lane * 16 < RS * blk_bytes;
-    dma16(in ? u.sr : u.snull, region + WAVE_W, in ? goff : 0);
+    dma16(u.sr, region + WAVE_W, in ? goff : OOB_OFF);
   }
   // this unit's rows: tile `tile` of the expert's rows (one pass)
   const int r_begin = tile * NT * 16;
@@ -720,8 +731,8 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
     for (int tt = 0; tt < NT; ++tt) xo[tt] = u.xoff(a, sl[tt]);
     uint4 areg[DA][4 * NT];
     auto load_a = [&](int p, int kbl) {  // zeros past the wave's range
-      const bool ok = kbl < u.nmy;
-      const int kb = ok ? u.lo + kbl : u.lo;
+      const bool ok = uni_b(kbl < u.nmy);
+      const int kb = uni_i(ok ? u.lo + kbl : u.lo);
 #pragma unroll
       for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -811,7 +822,7 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Route& rt,
   // LDS piece (row, c') holds source piece c' ^ (row & 3)
   const int dr = u.lane >> 2, dc = (u.lane & 3) ^ (dr & 3);
   auto copy_kb = [&](int kbl) {
-    const bool ok = kbl < u.nmy;
+    const bool ok = uni_b(kbl < u.nmy);
 #pragma unroll
     for (int rs = 0; rs < RS; ++rs)
       dma16(ok ? u.wr : u.wnull, kbuf(kbl) + rs * 1024,
@@ -828,7 +839,7 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Route& rt,
       goff = blk * G::ROWS_B * u.ng * 2 + u.lane * 16;
     }
     const bool in = u.lane * 16 < RS * blk_bytes;
-    dma16(in ? u.sr : u.snull, scl, in ? goff : 0);
+    dma16(u.sr, scl, in ? goff : OOB_OFF);
   }
   copy_kb(0);
   const int r_begin = tile * 16;
@@ -837,8 +848,8 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Route& rt,
   const int xo = u.xoff(a, sl[0]);
   uint4 areg[2][4];
   auto load_a = [&](int p, int kbl) {  // zeros past the wave's range
-    const bool ok = kbl < u.nmy;
-    const int kb = ok ? u.lo + kbl : u.lo;
+    const bool ok = uni_b(kbl < u.nmy);
+    const int kb = uni_i(ok ? u.lo + kbl : u.lo);
 #pragma unroll
     for (int d = 0; d < 4; ++d)
       areg[p][d] = __builtin_bit_cast(
@@ -934,7 +945,7 @@ __device__ __forceinline__ void run_unit_dma_chunked(const LayerArgs& a, const R
       const int rr = f / nd, d = f - (f / nd) * nd;
       const bool in = f < nflat;
       const int b0 = (u.row(a, blk, in ? rr : 0) * u.ng + g_lo) * 2;
-      dma4(in ? u.sr : u.snull, dst + i0 * 4, in ? (b0 & ~3) + d * 4 : 0);
+      dma4(u.sr, dst + i0 * 4, in ? (b0 & ~3) + d * 4 : OOB_OFF);
     }
   }
   const uint16_t* sc_lds = reinterpret_cast<const uint16_t*>(region + WAVE_W);
@@ -976,8 +987,8 @@ __device__ __forceinline__ void run_unit_dma_chunked(const LayerArgs& a, const R
       }
       uint4 areg[DA][4 * NT];
       auto load_a = [&](int p, int kbl) {  // zeros past the chunk
-        const bool ok = kbl < nc;
-        const int kb = ok ? u.lo + c0 + kbl : u.lo;
+        const bool ok = uni_b(kbl < nc);
+        const int kb = uni_i(ok ? u.lo + c0 + kbl : u.lo);
 #pragma unroll
         for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -1069,7 +1080,7 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
       const int rr = f / nd, d = f - (f / nd) * nd;
       const bool in = f < nflat;
       const int b0 = (u.row(a, blk, in ? rr : 0) * u.ng + g_lo) * 2;
-      dma4(in ? u.sr : u.snull, dst + i0 * 4, in ? (b0 & ~3) + d * 4 : 0);
+      dma4(u.sr, dst + i0 * 4, in ? (b0 & ~3) + d * 4 : OOB_OFF);
     }
     __builtin_amdgcn_sched_barrier(0);  // the copies go out before the ring loads
   }
@@ -1085,9 +1096,9 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
   uint4 areg[P][4 * NT];
   int xo[NT];
   auto load_w = [&](int p, int kbl) {
-    const bool ok = kbl < u.nmy;
+    const bool ok = uni_b(kbl < u.nmy);
     const __amdgpu_buffer_rsrc_t r = ok ? u.wr : u.wnull;
-    const int kb = ok ? u.lo + kbl : u.lo;
+    const int kb = uni_i(ok ? u.lo + kbl : u.lo);
 #pragma unroll
     for (int rs = 0; rs < RS; ++rs) {
 #pragma unroll
@@ -1097,8 +1108,8 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
     }
   };
   auto load_a = [&](int p, int kbl) {
-    const bool ok = kbl < u.nmy;
-    const int kb = ok ? u.lo + kbl : u.lo;
+    const bool ok = uni_b(kbl < u.nmy);
+    const int kb = uni_i(ok ? u.lo + kbl : u.lo);
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt)
 #pragma unroll
@@ -1263,13 +1274,19 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
     }
   }
   const int n_units = n_tiles * nb;
-  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {  // uniform across the work-group
-    const int t = __popcll(__ballot(incl_u <= u));  // segment = tile index
+  // unit u -> (expert, row block, k-split, tile); uniform across the work-group
+  auto decode = [&](int u, int& e, int& blk, int& sp, int& t) {
+    t = __popcll(__ballot(incl_u <= u));  // segment = tile index
     const int v = u - (t > 0 ? __builtin_amdgcn_readlane(incl_u, t - 1) : 0);
     const int ai = v / nb;
     const int bs = v - ai * nb;
-    const int blk = bs / ns, sp = bs - (bs / ns) * ns;
-    const int e = t == 0 ? select_expert(ai, word, incl, c) : select_tiled_expert(a, cntw, rt, t, ai);
+    blk = bs / ns;
+    sp = bs - blk * ns;
+    e = t == 0 ? select_expert(ai, word, incl, c) : select_tiled_expert(a, cntw, rt, t, ai);
+  };
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    int e, blk, sp, t;
+    decode(u, e, blk, sp, t);
     const int tier = MIXED ? __builtin_amdgcn_readfirstlane((int)a.tier[e]) : 2;
     if (!MIXED || tier == 2) {
       if constexpr (PATH == 1 && NT == 1 && !MIXED)
@@ -1343,6 +1360,8 @@ bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, i
   if (!(T >= 1 && T <= 64 && T * k <= MAX_SLOTS && Ep <= kDecodeMaxBuckets && n_shared <= 64 &&
         H / 32 <= kDecodeMaxHBlocks && H % 64 == 0 && gkb >= 1 && (gkb & (gkb - 1)) == 0))
     return false;
+  // the partial rows (every split) stay below the out-of-range offset
+  if ((int64_t)kDecodeMaxSplit * T * (k + n_shared) * H * 4 >= OOB_OFF) return false;
   // a register-ring unit's scales (rows x dwords of its widest k-range) fit in LDS
   auto ring_scales_fit = [&](int64_t K, int64_t rows) {
     const int64_t nkb = K / 128, span = (nkb + 3) / 4;
