@@ -124,3 +124,26 @@ def test_prefetched_int4_experts_feed_fused_layer(device):
     assert torch.equal(out, ref)
     cache.sync_prefetches(side)
     assert cache.stats["hits"] == E and cache.stats["misses"] == 0
+
+
+@pytest.mark.gpu
+def test_bounded_cache_evicts_and_refetches_on_gpu(device):
+    """LRU bound on the device: a dropped expert comes back from its pinned
+    host copy bit-identical, and the device bytes never exceed the bound."""
+    E, shape = 6, (64, 256)
+    ws = [torch.randn(shape, generator=torch.Generator().manual_seed(e)).to(torch.bfloat16)
+          for e in range(E)]
+    one = ws[0].numel() * ws[0].element_size()
+    cache = ExpertWeightCache({}, device=device, capacity_bytes=3 * one)
+    for e in range(E):
+        cache.register_expert(0, e, ws[e])
+    side = torch.cuda.Stream(device)
+    for rnd in range(2):
+        for e in range(E):
+            cache.prefetch(0, e, side)
+            assert cache.device_bytes <= 3 * one
+            got = cache.get(0, e)
+            assert torch.equal(got.cpu(), ws[e])
+    cache.sync_prefetches(side)
+    assert cache.evictions == 2 * E - 3
+    assert cache.stats["gpu_resident"] == 3 and cache.stats["hits"] == 2 * E
