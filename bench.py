@@ -482,8 +482,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}, "
-              f"WORLD_SIZE={world}); the expert-parallel sharding is design-only, see "
-              "DESIGN.md", file=sys.stderr)
+              f"WORLD_SIZE={world}); sharding the experts over GPUs (an all-to-all of "
+              "token rows before and after the expert kernels) is not built", file=sys.stderr)
         sys.exit(2)
     if args.pmc_summary:
         pmc_summary(args.pmc_summary)
