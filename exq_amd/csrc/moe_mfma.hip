@@ -534,8 +534,6 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
                      workspace_bytes, L.total);
   EXQ_REQUIRE(hidden && topk_ids && out && workspace, "%s: null pointer", fn);
   EXQ_REQUIRE(p->top_k == 0 || topk_weights, "%s: null topk_weights", fn);
-  EXQ_REQUIRE(p->n_shared == 0 || (!sort_order_out && !expert_ends_out),
-              "%s: routing copies are only produced without shared experts", fn);
   EXQ_REQUIRE(((uintptr_t)hidden | (uintptr_t)out | (uintptr_t)workspace) % 16 == 0,
               "%s: hidden, out and workspace must be 16-byte aligned", fn);
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);

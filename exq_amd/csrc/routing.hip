@@ -212,6 +212,13 @@ __device__ __forceinline__ int plan_key(const RoutePlanParams& p, int slot) {
   return p.E + (j - p.k);
 }
 
+// Flat routed slot t*k + j of plan slot t*kp + j (j < k): the index space of
+// sort_order_out, which lists the routed experts' slots only.
+__device__ __forceinline__ int64_t routed_slot(const RoutePlanParams& p, int slot) {
+  const int t = slot / p.kp;
+  return (int64_t)t * p.k + (slot - t * p.kp);
+}
+
 // Everything after the sort that needs only the bucket counts s.cnt and
 // starts s.start (one work-group): boundaries, token groups (tier order BF16,
 // INT8, INT4, so long work items start early), header, combine counters, and
@@ -275,9 +282,9 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
   }
   if (threadIdx.x == 0) s.start[nb] = t;
   __syncthreads();
-  stable_scatter(p.n, nb, key, s.run, s.masks, [&](int i, int, int pos) {
+  stable_scatter(p.n, nb, key, s.run, s.masks, [&](int i, int b, int pos) {
     p.sorted[pos] = i;
-    if (p.sort_order_out) p.sort_order_out[pos] = i;
+    if (p.sort_order_out && b < p.E) p.sort_order_out[pos] = routed_slot(p, i);
   });
   plan_tail(p, s);
 }
@@ -329,9 +336,9 @@ __global__ void __launch_bounds__(RT) route_scatter_kernel(RoutePlanParams p) {
   for (int e = threadIdx.x; e < nb; e += RT) s.run[e] = p.blk_cnt[(int64_t)blockIdx.x * nb + e];
   __syncthreads();
   stable_scatter(m, nb, [&](int i) { return plan_key(p, lo + i); }, s.run, s.masks,
-                 [&](int i, int, int pos) {
+                 [&](int i, int b, int pos) {
                    p.sorted[pos] = lo + i;
-                   if (p.sort_order_out) p.sort_order_out[pos] = lo + i;
+                   if (p.sort_order_out && b < p.E) p.sort_order_out[pos] = routed_slot(p, lo + i);
                  });
 }
 

@@ -39,10 +39,32 @@ def _problem(hidden: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.T
 def _check_routing(hidden, topk_weights, topk_ids):
     if hidden.dim() != 2:
         raise ValueError("hidden_states must be [T, H]")
-    if topk_ids.shape != topk_weights.shape or topk_ids.shape[0] != hidden.shape[0]:
+    if (topk_ids.dim() != 2 or topk_ids.shape != topk_weights.shape
+            or topk_ids.shape[0] != hidden.shape[0]):
         raise ValueError("topk_ids / topk_weights must both be [T, k]")
     if hidden.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("hidden_states must be float16 or bfloat16")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise ValueError("topk_ids must be int32 or int64")
+    if topk_weights.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError("topk_weights must be float32, float16 or bfloat16")
+
+
+def _check_outputs(hidden, topk_ids, n_experts, out, sort_order_out, expert_ends_out):
+    """Caller-supplied output buffers are written through raw pointers by the
+    kernels, so their sizes and dtypes are checked here, before any launch."""
+    T, H = hidden.shape
+    if out is not None and (tuple(out.shape) != (T, H) or out.dtype != hidden.dtype):
+        raise ValueError(f"out must be [{T}, {H}] with dtype {hidden.dtype}")
+    if sort_order_out is not None and (sort_order_out.dtype != torch.int64
+                                       or sort_order_out.numel() != topk_ids.numel()):
+        raise ValueError(f"sort_order_out must be int64 with {topk_ids.numel()} elements")
+    if expert_ends_out is not None and (expert_ends_out.dtype != torch.int32
+                                        or expert_ends_out.numel() != n_experts + 1):
+        raise ValueError(f"expert_ends_out must be int32 with {n_experts + 1} elements")
+    for t in (out, sort_order_out, expert_ends_out):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("output buffers must be contiguous")
 
 
 def fused_experts(hidden_states: torch.Tensor, w13_packed: torch.Tensor,
@@ -68,20 +90,28 @@ def fused_experts(hidden_states: torch.Tensor, w13_packed: torch.Tensor,
     if activation != "silu":
         raise ValueError(f"unsupported activation {activation!r} (only 'silu')")
     _check_routing(hidden_states, topk_weights, topk_ids)
-    dev = _lib.require_gpu(hidden_states, w13_packed, w13_scales, w2_packed, w2_scales,
-                           topk_weights, topk_ids, out, sort_order_out, expert_ends_out)
     T, H = hidden_states.shape
+    if w13_packed.dim() != 3 or w2_packed.dim() != 3:
+        raise ValueError("packed weights must be [E, N, K/2]")
     E, two_i, h2 = w13_packed.shape
     I = two_i // 2
-    if h2 * 2 != H or w2_packed.shape != (E, H, I // 2):
+    if h2 * 2 != H or tuple(w2_packed.shape) != (E, H, I // 2):
         raise ValueError("packed weight shapes do not match hidden / intermediate sizes")
+    if w13_packed.dtype != torch.uint8 or w2_packed.dtype != torch.uint8:
+        raise ValueError("packed weights must be uint8")
+    if w13_scales.dtype != torch.float16 or w2_scales.dtype != torch.float16:
+        raise ValueError("INT4 scales must be float16")
+    _check_outputs(hidden_states, topk_ids, E, out, sort_order_out, expert_ends_out)
     gs = _effective_group(H, w13_scales)
     if _effective_group(I, w2_scales) != gs:
         raise ValueError("w13 and w2 must use the same group size")
+    if (tuple(w13_scales.shape) != (E, two_i, H // gs)
+            or tuple(w2_scales.shape) != (E, H, I // gs)):
+        raise ValueError("scale shapes do not match the packed weights")
+    dev = _lib.require_gpu(hidden_states, w13_packed, w13_scales, w2_packed, w2_scales,
+                           topk_weights, topk_ids, out, sort_order_out, expert_ends_out)
     if out is None:
         out = torch.empty(T, H, dtype=hidden_states.dtype, device=dev)
-    elif out.shape != (T, H) or out.dtype != hidden_states.dtype:
-        raise ValueError("out must be [T, H] with the activation dtype")
     p = _problem(hidden_states, topk_ids, topk_weights, E, I, gs)
     L = _lib.lib()
     need = L.exq_moe_workspace_size(p)
@@ -241,12 +271,15 @@ def fused_experts_mixed(hidden_states: torch.Tensor, bank: MixedExpertBank,
                         workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Mixed BF16/INT8/INT4 MoE layer (plus shared experts) in one launch sequence."""
     _check_routing(hidden_states, topk_weights, topk_ids)
-    dev = _lib.require_gpu(hidden_states, topk_weights, topk_ids, out, *bank.tensors())
     T, H = hidden_states.shape
     if H != bank.hidden_size:
         raise ValueError("hidden size does not match the bank")
     if bank.bf16_w13 is not None and bank.bf16_w13.dtype != hidden_states.dtype:
         raise ValueError("BF16-tier weights must have the activation dtype")
+    _check_outputs(hidden_states, topk_ids, bank.n_experts, out, sort_order_out,
+                   expert_ends_out)
+    dev = _lib.require_gpu(hidden_states, topk_weights, topk_ids, out, sort_order_out,
+                           expert_ends_out, *bank.tensors())
     if out is None:
         out = torch.empty(T, H, dtype=hidden_states.dtype, device=dev)
     p = _problem(hidden_states, topk_ids, topk_weights, bank.n_experts, bank.inter_size,

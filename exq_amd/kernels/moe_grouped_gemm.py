@@ -77,19 +77,28 @@ def moe_grouped_gemm(hidden_states: torch.Tensor, expert_weights: torch.Tensor,
 
 
 def unsort_output(sorted_output: torch.Tensor, router_indices: torch.Tensor,
-                  router_weights: torch.Tensor) -> torch.Tensor:
-    """Undo the stable sort and take the router-weighted sum over top-k.
+                  router_weights: torch.Tensor, n_experts: int | None = None) -> torch.Tensor:
+    """Undo the stable sort and take the router-weighted sum over top-k
+    (the reference's unsort_output, moe_grouped_gemm.py:234-260).
 
-    Returns ``[n_tokens, N]`` in ``sorted_output``'s dtype.
+    Returns ``[n_tokens, N]`` in ``sorted_output``'s dtype.  The inverse
+    permutation comes from the same stable dispatch sort as
+    ``moe_grouped_gemm`` (so the two compose), with no device->host read:
+    ``n_experts`` bounds the ids (default 1023, the dispatch kernel's largest
+    bucket count); ids in ``[0, n_experts)`` give exactly the reference's
+    ``torch.argsort(ids, stable=True)`` order.
     """
-    dev = _lib.require_gpu(sorted_output)
+    dev = _lib.require_gpu(sorted_output, router_indices, router_weights)
     T, k = router_indices.shape
     n = T * k
+    if sorted_output.dim() != 2 or sorted_output.shape[0] != n:
+        raise ValueError(f"sorted_output must be [{n}, N]")
+    E = 1023 if n_experts is None else int(n_experts)
     ids = router_indices.reshape(-1).contiguous()
     sort_order = torch.empty(n, dtype=torch.int64, device=dev)
     sorted_ids = torch.empty(n, dtype=torch.int64, device=dev)
-    ends = torch.empty(int(ids.max().item()) + 2 if n else 1, dtype=torch.int32, device=dev)
-    dispatch(ids, sort_order, sorted_ids, ends, ends.numel() - 1)
+    ends = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    dispatch(ids, sort_order, sorted_ids, ends, E)
     result = torch.empty(T, sorted_output.shape[1], dtype=sorted_output.dtype, device=dev)
     combine(sorted_output.contiguous(), sort_order, router_weights.contiguous(), result)
     return result

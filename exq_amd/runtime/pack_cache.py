@@ -25,7 +25,7 @@ from typing import Callable
 
 import torch
 
-FORMAT_VERSION = 1
+FORMAT_VERSION = 2
 _TENSORS = ("w13_packed", "w13_scales", "w2_packed", "w2_scales")
 
 
@@ -43,7 +43,7 @@ def fingerprint(*weights: torch.Tensor, sample_rows: int = 64) -> str:
         rows = torch.linspace(0, N - 1, min(sample_rows, N)).round().long().to(w.device)
         sample = w.index_select(1, rows).contiguous()
         h.update(sample.view(torch.uint8).cpu().numpy().tobytes())
-        h.update(repr(float(w.double().sum().item())).encode())
+        h.update(repr(float(w.sum(dtype=torch.float64).item())).encode())
     return h.hexdigest()
 
 

@@ -90,6 +90,7 @@ def _exq_forward_cuda(self_method, layer, dispatch_output, _original_forward_cud
         return _original_forward_cuda(self_method, layer, dispatch_output)
 
     hidden = dispatch_output.hidden_states
+    in_dtype = hidden.dtype
     topk = dispatch_output.topk_output
     cache = _get_or_pack(layer, backend)
     if hidden.dtype not in (torch.float16, torch.bfloat16):
@@ -105,6 +106,8 @@ def _exq_forward_cuda(self_method, layer, dispatch_output, _original_forward_cud
         if bank.bf16_w13 is not None and bank.bf16_w13.dtype != hidden.dtype:
             hidden = hidden.to(bank.bf16_w13.dtype)
         out = fused_experts_mixed(hidden, bank, wts, ids)
+    if out.dtype != in_dtype:  # the caller's activation dtype, whatever the bank stores
+        out = out.to(in_dtype)
     return StandardCombineInput(hidden_states=out)
 
 

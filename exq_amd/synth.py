@@ -115,6 +115,35 @@ def mixed_tiers(n_experts: int, seed: int, bf16_frac: float = 0.1,
     return tiers
 
 
+def router_tiers(cfg: MoeConfig, layer: int = 0, bf16_frac: float = 0.1,
+                 int8_frac: float = 0.2) -> list[int]:
+    """Per-expert tiers of a layer ranked by the router's own Zipf activation
+    frequencies (the permutation ``router_logits`` draws first for this layer):
+    the most frequently routed 10% BF16 (0), the next 20% INT8 (1), the rest
+    INT4 (2), so the hot tier is the set of experts the router favours."""
+    rng = np.random.default_rng(seed_for(cfg, layer) + 7)
+    freq = np.exp(zipf_bias(cfg.n_experts, rng))
+    order = np.argsort(-freq, kind="stable")
+    n_bf = int(round(bf16_frac * cfg.n_experts))
+    n_i8 = int(round(int8_frac * cfg.n_experts))
+    tiers = [2] * cfg.n_experts
+    for r, e in enumerate(order):
+        tiers[int(e)] = 0 if r < n_bf else (1 if r < n_bf + n_i8 else 2)
+    return tiers
+
+
+def plan_artifact(cfg: MoeConfig, n_layers: int | None = None) -> dict:
+    """Quant-plan artifact of the mixed stack in the reference's format
+    (``quant_assignments`` {"L:E": "BF16" | "INT8" | "INT4"}), tiers from
+    ``router_tiers`` of each layer."""
+    names = {0: "BF16", 1: "INT8", 2: "INT4"}
+    qa = {}
+    for l in range(cfg.n_layers if n_layers is None else n_layers):
+        for e, t in enumerate(router_tiers(cfg, l)):
+            qa[f"{l}:{e}"] = names[t]
+    return {"model": f"synthetic-{cfg.name}", "quant_assignments": qa}
+
+
 def int4_expert_bytes(H: int, I: int, g: int = 128) -> int:
     return 3 * H * I // 2 + 2 * (2 * I * (H // g) + H * (I // g))
 

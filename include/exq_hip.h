@@ -261,7 +261,9 @@ size_t exq_moe_workspace_size(const exq_moe_problem* problem);
  * silu_and_mul -> GEMM2 -> combine) and moe_int4_full_forward
  * (exq/kernels/moe_int4_kernel.py:330-426).  No host synchronisation.
  * sort_order_out [T*k] (i64) and expert_ends_out [E+1] (i32) are optional
- * copies of the routing preparation (only when n_shared == 0).
+ * copies of the routing preparation over the routed experts: sort_order_out
+ * lists routed slots t*k + j (shared experts are not in it), the entries past
+ * expert_ends_out[E] are left unwritten (slots whose id is outside [0, E)).
  */
 int exq_moe_int4_fused_forward(const exq_moe_problem* problem, const void* hidden,
                                const void* topk_ids, const void* topk_weights,

@@ -41,17 +41,3 @@ def tier_fallback_freqs(tiers: np.ndarray) -> np.ndarray:
     """exq_artifact.py:168-173: BF16 0.15, INT8 0.05, INT4 0.01."""
     lut = np.array([0.15, 0.05, 0.01], dtype=np.float32)
     return lut[tiers.astype(np.int64)]
-
-
-def classify_precision(freq: float, n_experts: int, top_k: int) -> str:
-    """Quant-plan classifier (quant_planner.rs:95-103) with the automatic
-    thresholds hot = 2k/N, warm = k/(2N) (graph_analysis thresholds cited by
-    the survey).  Used only to build synthetic plans.
-    """
-    hot = 2.0 * top_k / n_experts
-    warm = top_k / (2.0 * n_experts)
-    if freq >= hot:
-        return "BF16"
-    if freq >= warm:
-        return "INT8"
-    return "INT4"

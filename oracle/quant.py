@@ -42,7 +42,8 @@ def pack_int4_weights(weights: np.ndarray, group_size: int = 128):
     pinned by: hand-derived known answers (byte 0x1F for w=[1,-1], half-even
     ties 2.5->2 and 3.5->4, the zero-row scale fp16(2^-23)), the invariants
     nibble in [1,15] and |w - deq| <= scale/2, and an element-by-element
-    Python brute force on tiny inputs (tests/test_oracle_quant.py).
+    Python brute force on tiny inputs, g = 128, the K < g collapse and g = 32
+    (tests/test_oracle_quant.py::test_pack_matches_elementwise_brute_force).
     """
     w = np.asarray(weights)
     N, K = w.shape
@@ -81,17 +82,20 @@ def dequant_int4(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
     pinned by: round trip against pack_int4_weights known answers and the
     bound |w - deq| <= scale/2 (tests/test_oracle_quant.py).
     """
-    p = np.asarray(packed).astype(np.uint8)
+    p = np.asarray(packed).astype(np.uint8, copy=False)
     s = np.asarray(scales).astype(np.float32)
     K = p.shape[-1] * 2
-    g = K // s.shape[-1]
-    lo = (p & 0x0F).astype(np.float32) - 8.0
-    hi = ((p >> 4) & 0x0F).astype(np.float32) - 8.0
-    w = np.empty(p.shape[:-1] + (K,), dtype=np.float32)
-    w[..., 0::2] = lo
-    w[..., 1::2] = hi
-    s_full = np.repeat(s, g, axis=-1)
-    return (w * s_full).astype(np.float32)
+    ng = s.shape[-1]
+    g = K // ng
+    # byte -> (low nibble - 8, high nibble - 8): one table lookup per byte puts
+    # the even-k and odd-k values side by side in k order
+    w = _NIBBLE_PAIRS[p].reshape(p.shape[:-1] + (ng, g))
+    w *= s[..., None]
+    return w.reshape(p.shape[:-1] + (K,))
+
+
+_NIBBLE_PAIRS = np.stack([(np.arange(256) & 0x0F) - 8.0, (np.arange(256) >> 4) - 8.0],
+                         axis=-1).astype(np.float32)
 
 
 def quantize_int8(weights: np.ndarray):
@@ -116,7 +120,11 @@ def quantize_int8(weights: np.ndarray):
 
 
 def dequant_int8(q: np.ndarray, scales: np.ndarray) -> np.ndarray:
-    """q * float(fp16 per-row scale) in float32 (exact products)."""
+    """q * float(fp16 per-row scale) in float32 (exact products).
+
+    pinned by: known answers with distinct per-row scales, 2-D and batched
+    (tests/test_oracle_quant.py::test_dequant_int8_per_row_scales_known_answer).
+    """
     return (np.asarray(q).astype(np.float32)
             * np.asarray(scales).astype(np.float32)[..., None]).astype(np.float32)
 

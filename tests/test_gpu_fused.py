@@ -219,7 +219,10 @@ def test_moe_int4_forward_sorted_output(device):
     so, sh, ends, max_tok = sort_tokens_by_expert(tid, x, cfg.n_experts)
     r_so, r_ends, r_max = routing.sort_tokens_by_expert(ids, cfg.n_experts)
     assert np.array_equal(so.cpu().numpy(), r_so) and max_tok == r_max
+    assert np.array_equal(ends.cpu().numpy(), r_ends)
     a = moe.gather_hidden(x.float().cpu().numpy(), r_so, cfg.top_k)
+    # the gathered rows are copies: bit-exact
+    assert np.array_equal(sh.float().cpu().numpy(), a)
     wdq = quant.dequant_int4(p13.cpu().numpy(), s13.cpu().numpy())
     ref = moe.grouped_gemm_sorted(a, wdq, r_ends)
     assert_close_rel(out, ref, TOL, "moe_int4_forward")
@@ -263,3 +266,42 @@ def test_fused_duplicate_ids_randint_routing(T, device):
                         torch.from_numpy(ids).to(device))
     ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
     assert_close_rel(out, ref, TOL, f"duplicate ids T={T}")
+
+
+def test_unsort_output_inverts_grouped_gemm(device):
+    """unsort_output(moe_grouped_gemm(...)) is the reference's
+    pytorch_moe_reference composition (moe_grouped_gemm.py:234-290): the
+    inverse of the stable sort plus the router-weighted sum over top-k."""
+    from exq_amd.kernels import moe_grouped_gemm, unsort_output
+    from oracle import moe
+    banner("unsort_output")
+    rng = np.random.default_rng(4)
+    E, N, K, T, k = 6, 64, 256, 13, 3
+    W = torch.from_numpy((rng.standard_normal((E, N, K)) * 0.05).astype(np.float32))
+    ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)])
+    wts = rng.random((T, k)).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(torch.bfloat16)
+    tid = torch.from_numpy(ids).to(device)
+    sorted_out = moe_grouped_gemm(x.to(device), W.to(torch.bfloat16).to(device), tid, E)
+    # independent of any sort: out[t] = sum_j w[t, j] * (x[t] @ W[ids[t, j]]^T)
+    xf, Wf = x.float().numpy().astype(np.float64), W.to(torch.bfloat16).float().numpy()
+    ref = np.zeros((T, N))
+    for t in range(T):
+        for j in range(k):
+            ref[t] += wts[t, j] * (Wf[ids[t, j]] @ xf[t])
+    for n_exp in (None, E):
+        out = unsort_output(sorted_out, tid, torch.from_numpy(wts).to(device), n_exp)
+        assert_close_rel(out, ref, TOL, f"unsort_output n_experts={n_exp}")
+
+
+def test_moe_int4_full_forward_delegate(device):
+    from exq_amd.kernels import moe_int4_full_forward
+    banner("moe_int4_full_forward")
+    cfg = MID
+    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, 12, device)
+    ids, w, tid, tw = _routing(cfg, 9, device)
+    x = _hidden(9, cfg.hidden, 3, device)
+    out = moe_int4_full_forward(x, p13, s13, p2, s2, tid, tw, cfg.n_experts)
+    assert out.shape == (9, cfg.hidden) and out.dtype == x.dtype
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, "moe_int4_full_forward")

@@ -197,3 +197,102 @@ def test_sglang_patch_unpatch_and_fallback(tmp_path, monkeypatch):
     sb.patch_sglang(path)  # re-patch keeps the true original
     sb.unpatch_sglang()
     assert cls.forward_cuda is orig and not cls._exq_patched
+
+
+def _cpu_layer(T=4, H=256, I=128, E=4, k=2):
+    x = torch.zeros(T, H, dtype=torch.bfloat16)
+    p13 = torch.zeros(E, 2 * I, H // 2, dtype=torch.uint8)
+    s13 = torch.zeros(E, 2 * I, H // 128, dtype=torch.float16)
+    p2 = torch.zeros(E, H, I // 2, dtype=torch.uint8)
+    s2 = torch.zeros(E, H, I // 128, dtype=torch.float16)
+    ids = torch.zeros(T, k, dtype=torch.int64)
+    w = torch.zeros(T, k, dtype=torch.float32)
+    return x, p13, s13, p2, s2, w, ids
+
+
+@pytest.mark.parametrize("bad", ["out_shape", "out_dtype", "so_dtype", "so_size", "ends_dtype",
+                                 "ends_size", "ids_dtype", "scale_shape"])
+def test_fused_wrappers_reject_bad_buffers_before_launch(bad):
+    """Output buffers the kernels write through raw pointers are checked on the
+    host (ValueError) before the device check or any launch."""
+    from exq_amd.kernels import fused_experts
+    x, p13, s13, p2, s2, w, ids = _cpu_layer()
+    kw = {}
+    if bad == "out_shape":
+        kw["out"] = torch.empty(3, 256, dtype=torch.bfloat16)
+    elif bad == "out_dtype":
+        kw["out"] = torch.empty(4, 256, dtype=torch.float16)
+    elif bad == "so_dtype":
+        kw["sort_order_out"] = torch.empty(8, dtype=torch.int32)
+    elif bad == "so_size":
+        kw["sort_order_out"] = torch.empty(7, dtype=torch.int64)
+    elif bad == "ends_dtype":
+        kw["expert_ends_out"] = torch.empty(5, dtype=torch.int64)
+    elif bad == "ends_size":
+        kw["expert_ends_out"] = torch.empty(4, dtype=torch.int32)
+    elif bad == "ids_dtype":
+        ids = ids.to(torch.int16)
+    elif bad == "scale_shape":
+        s13 = s13[:, :, :1].contiguous().repeat(1, 1, 3)
+    with pytest.raises(ValueError):
+        fused_experts(x, p13, s13, p2, s2, w, ids, **kw)
+
+
+def test_fused_wrappers_accept_good_buffers_up_to_the_device_check():
+    from exq_amd import ExqError
+    from exq_amd.kernels import fused_experts
+    x, p13, s13, p2, s2, w, ids = _cpu_layer()
+    with pytest.raises(ExqError, match="HIP device"):
+        fused_experts(x, p13, s13, p2, s2, w, ids, out=torch.empty(4, 256, dtype=torch.bfloat16),
+                      sort_order_out=torch.empty(8, dtype=torch.int64),
+                      expert_ends_out=torch.empty(5, dtype=torch.int32))
+
+
+def test_mixed_wrapper_rejects_bad_out():
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    x, *_, w, ids = _cpu_layer()
+    bank = MixedExpertBank(n_experts=4, n_shared=0, hidden_size=256, inter_size=128,
+                           group_size=128, tier=torch.full((4,), 2, dtype=torch.int8),
+                           index=torch.arange(4, dtype=torch.int32))
+    with pytest.raises(ValueError, match="out must be"):
+        fused_experts_mixed(x, bank, w, ids, out=torch.empty(4, 256, dtype=torch.float16))
+    with pytest.raises(ValueError, match="sort_order_out"):
+        fused_experts_mixed(x, bank, w, ids, sort_order_out=torch.empty(8, dtype=torch.int32))
+    with pytest.raises(ValueError, match="expert_ends_out"):
+        fused_experts_mixed(x, bank, w, ids, expert_ends_out=torch.empty(6, dtype=torch.int32))
+
+
+def test_pack_cache_fingerprint_uses_no_float64_copy():
+    """The fingerprint's exact sum reduces in float64 without materialising a
+    float64 copy of the bank (w.sum(dtype=float64)); a changed element changes it."""
+    from exq_amd.runtime.pack_cache import fingerprint
+    w = torch.randn(2, 16, 256, dtype=torch.float32).to(torch.bfloat16)
+    f0 = fingerprint(w)
+    assert f0 == fingerprint(w.clone())
+    w2 = w.clone()
+    w2[1, 7, 3] += 1
+    assert fingerprint(w2) != f0
+    src = (ROOT / "exq_amd" / "runtime" / "pack_cache.py").read_text()
+    assert "sum(dtype=torch.float64)" in src and ".double()" not in src
+
+
+def test_mixed_plan_hot_tier_is_the_routers_favoured_experts(tmp_path):
+    """The mixed stack's BF16 tier is the experts the router sends most slots
+    to, and the plan round-trips through the artifact reader."""
+    from exq_amd import synth
+    from exq_amd.kernels import load_exq_artifact
+    cfg = synth.CONFIGS["mixed_olmoe"]
+    art = synth.plan_artifact(cfg, 2)
+    path = tmp_path / "plan.json"
+    path.write_text(json.dumps(art))
+    prof = load_exq_artifact(str(path), device="cpu")
+    for l in range(2):
+        tiers = synth.router_tiers(cfg, l)
+        assert prof.tiers[l].tolist() == tiers
+        assert tiers.count(0) == 6 and tiers.count(1) == 13 and tiers.count(2) == 45
+        ids, _ = synth.routing(cfg, 4096, l)
+        counts = np.bincount(ids.reshape(-1), minlength=64)
+        bf = [e for e in range(64) if tiers[e] == 0]
+        i4 = [e for e in range(64) if tiers[e] == 2]
+        # hot experts take far more slots than the INT4 tail on average
+        assert counts[bf].mean() > 4 * counts[i4].mean()

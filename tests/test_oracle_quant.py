@@ -112,3 +112,52 @@ def test_fake_quant_int4_zero_rows_and_agreement():
     deq = quant.dequant_int4(p, s)
     # same integers; only the fp16 rounding of the scale differs (<= 2^-11 rel)
     assert np.allclose(fq, deq, rtol=2e-3, atol=1e-6)
+
+
+def _brute_pack_row(row, g):
+    """Element-by-element restatement of pack_int4_weights for one row: scale per
+    group from a Python max over |w|, q by Python's round-half-even, nibbles
+    placed one byte at a time (low nibble = even k)."""
+    K = len(row)
+    eps = float(np.finfo(np.float32).eps)
+    out, scales = [], []
+    for g0 in range(0, K, g):
+        grp = [np.float32(v) for v in row[g0:g0 + g]]
+        amax = np.float32(0.0)
+        for v in grp:
+            amax = max(amax, np.float32(abs(v)))
+        s = np.float32(max(np.float32(amax / np.float32(7.0)), np.float32(eps)))
+        scales.append(np.float16(s))
+        qs = []
+        for v in grp:
+            q = round(float(np.float32(v / s)))  # Python round() is half-even
+            qs.append(min(7, max(-8, q)))
+        for i in range(0, len(qs), 2):
+            out.append((qs[i] + 8) | ((qs[i + 1] + 8) << 4))
+    return out, scales
+
+
+@pytest.mark.parametrize("N,K,g,seed", [(3, 256, 128, 11), (2, 64, 128, 12), (4, 96, 32, 13)])
+def test_pack_matches_elementwise_brute_force(N, K, g, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float16)
+    w[0, :8] = np.float16(0.0)  # a partly zero group
+    packed, scales = quant.pack_int4_weights(w, group_size=g)
+    geff = quant.effective_group_size(K, g)
+    for r in range(N):
+        bp, bs = _brute_pack_row(w[r], geff)
+        assert packed[r].tolist() == bp
+        assert scales[r].view(np.uint16).tolist() == np.array(bs, np.float16).view(np.uint16).tolist()
+
+
+def test_dequant_int8_per_row_scales_known_answer():
+    # rows carry different fp16 scales: a per-row broadcast mix-up changes the answer
+    q = np.array([[1, -2, 127], [-128, 3, 0]], dtype=np.int8)
+    s = np.array([0.5, 0.25], dtype=np.float16)
+    deq = quant.dequant_int8(q, s)
+    assert deq.tolist() == [[0.5, -1.0, 63.5], [-32.0, 0.75, 0.0]]
+    # batched [E, N, K] with [E, N] scales
+    qq = np.stack([q, q[::-1]])
+    ss = np.stack([s, np.array([2.0, 4.0], np.float16)])
+    d2 = quant.dequant_int8(qq, ss)
+    assert d2[1].tolist() == [[-256.0, 6.0, 0.0], [4.0, -8.0, 508.0]]

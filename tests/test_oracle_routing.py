@@ -94,3 +94,32 @@ def test_softmax_topk_brute_force():
         assert ids[t].tolist() == ref
         assert abs(w[t].sum() - 1.0) < 1e-6
     assert ids[0, 0] == 3 and ids[0, 1] == 7
+
+
+@pytest.mark.parametrize("T,k,E,B,seed", [(16, 8, 64, 16, 7), (3, 2, 5, 4, 8)])
+def test_align_contract_the_reference_consumer_relies_on(T, k, E, B, seed):
+    """What the reference's call site and consumer fix about the padded layout
+    (sglang_backend.py:102-109 sizes the buffers n + (E+1)(B-1) and
+    ceil(./B); exq_dispatch.cu:83-96 counts an entry only when slot < n_active):
+    every padding entry is >= n_active, every real slot appears exactly once,
+    and the block count covers num_tokens_post_pad.  The +1 bucket shift and
+    the expert_ids fill past the end are sgl_kernel conventions outside this
+    contract."""
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)])
+    n = T * k
+    sorted_ids, expert_ids, ntpp, cumsum = routing.moe_align_block_size(ids, E + 1, B)
+    assert len(sorted_ids) == n + (E + 1) * (B - 1)
+    assert len(expert_ids) == -(-len(sorted_ids) // B)
+    real = sorted_ids[sorted_ids < n]
+    assert sorted(real.tolist()) == list(range(n))
+    pad_mask = np.ones(len(sorted_ids), bool)
+    pad_mask[np.isin(sorted_ids, real)] = False
+    assert np.all(sorted_ids[pad_mask] >= n)
+    assert int(ntpp[0]) <= len(sorted_ids) and int(ntpp[0]) % B == 0
+    # every block before num_tokens_post_pad names the expert of its real slots
+    flat = ids.reshape(-1)
+    for blk in range(int(ntpp[0]) // B):
+        ent = sorted_ids[blk * B:(blk + 1) * B]
+        ent = ent[ent < n]
+        assert all(flat[s] == expert_ids[blk] for s in ent)
