@@ -65,6 +65,7 @@ _SIGNATURES = {
     "exq_moe_workspace_size": ([C.POINTER(MoeProblem)], _SZ),
     "exq_moe_int4_fused_forward": ([C.POINTER(MoeProblem), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P], _INT),
     "exq_moe_mixed_forward": ([C.POINTER(MoeProblem), _P, _P, _P, C.POINTER(ExpertBank), _P, _P, _P, _P, _SZ, _P], _INT),
+    "exq_moe_int4_fused_forward_noalloc": ([C.POINTER(MoeProblem), _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P], _INT),
     "exq_set_stage_events": ([C.POINTER(C.c_void_p), _INT], _INT),
     "exq_pack_int4": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P], _INT),
     "exq_quantize_int8": ([_P, _INT, _I64, _I64, _P, _P, _P], _INT),

@@ -286,6 +286,27 @@ int exq_moe_mixed_forward(const exq_moe_problem* problem, const void* hidden,
                           void* workspace, size_t workspace_bytes, exq_stream stream);
 
 /*
+ * The INT4 layer of exq_moe_int4_fused_forward without a workspace argument:
+ * no counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Its scratch is a device array of
+ * EXQ_NOALLOC_SCRATCH_BYTES held by every GPU the library runs on until the
+ * process ends; a problem whose exq_moe_workspace_size exceeds it is rejected
+ * with EXQ_ERROR_WORKSPACE_TOO_SMALL before any launch.  The call allocates
+ * nothing (no hipMalloc / hipFree).  Every call on one GPU shares that GPU's
+ * scratch, so calls that may overlap on one GPU (other streams, other
+ * threads) race: serialise them.  Each call first clears the part of the
+ * scratch that must start at zero.  Same arguments and results otherwise.
+ */
+#define EXQ_NOALLOC_SCRATCH_BYTES (64u << 20)
+int exq_moe_int4_fused_forward_noalloc(const exq_moe_problem* problem, const void* hidden,
+                                       const void* topk_ids, const void* topk_weights,
+                                       const uint8_t* w13_packed, const uint16_t* w13_scales,
+                                       const uint8_t* w2_packed, const uint16_t* w2_scales,
+                                       void* out, int64_t* sort_order_out,
+                                       int32_t* expert_ends_out, exq_stream stream);
+
+/*
  * Measurement hook (no counterpart in the reference, whose harness times whole
  * calls with perf_counter, exq/eval/bench.py:15-46).  When set on the calling
  * thread, the next fused / mixed forward records hipEvent_t events on the
