@@ -40,8 +40,10 @@
 // accesses; every storing wave waits for its stores before its work-group
 // bumps the column block's counter, so no whole-cache writeback or
 // invalidate is needed (on this part agent-scope fences write back /
-// invalidate the whole L2 of an XCD).  The last combine zeroes the counters,
-// so the sync region is zero again when the launch ends.
+// invalidate the whole L2 of an XCD).  The gate/up kernel, which always runs
+// first on the same stream, zeroes the down kernel's counters, so the
+// workspace needs no zero fill and an interrupted call leaves nothing behind
+// for the next one; the last combine zeroes them again as well.
 #include "exq_internal.h"
 
 #include <hip/hip_ext.h>
@@ -1089,6 +1091,12 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
   // its slices in static arrays and has only this in dynamic LDS)
   uint32_t* cntw =
       reinterpret_cast<uint32_t*>(dyn_lds + (PATH == 1 && NT == 1 && !MIXED ? 0 : DW * WAVE_LDS));
+  if constexpr (PH == 0) {
+    // the down launch that follows on this stream starts from zero counters,
+    // whatever an earlier call (or the caller's fill) left in the workspace
+    for (int i = blockIdx.x * DNT + threadIdx.x; i <= kDecodeMaxHBlocks; i += gridDim.x * DNT)
+      __hip_atomic_store(sync_c(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   uint32_t word;
   int incl, c;
   const int n_active = route(a, rt, cntw, word, incl, c);

@@ -7,9 +7,9 @@
 // is looked up once per device with hipGetSymbolAddress and kept), from
 // module load until the process ends.  Every call on one GPU shares that
 // GPU's array: calls that overlap on one GPU (two streams, two threads) race
-// on it.  The array keeps the last call's contents, so each call clears the
-// region that must start at zero (the decode kernels' combine counters) with
-// a fill kernel on its own stream before the layer's kernels.
+// on it.  The array keeps the last call's contents; the only part that must
+// start at zero, the decode kernels' combine counters, is cleared by each
+// call's first kernel (as for any caller workspace).
 #include "exq_internal.h"
 
 #include <mutex>
@@ -44,11 +44,6 @@ int scratch_address(void** out) {
   return EXQ_SUCCESS;
 }
 
-__global__ void __launch_bounds__(256) clear_kernel(uint4* p, int n16) {
-  for (int i = blockIdx.x * 256 + threadIdx.x; i < n16; i += gridDim.x * 256)
-    p[i] = uint4{0u, 0u, 0u, 0u};
-}
-
 }  // namespace
 }  // namespace exq
 
@@ -69,13 +64,7 @@ extern "C" int exq_moe_int4_fused_forward_noalloc(
                      fn, need, (size_t)EXQ_NOALLOC_SCRATCH_BYTES);
   if (problem->n_tokens == 0) return EXQ_SUCCESS;
   void* ws = nullptr;
-  int st = scratch_address(&ws);
-  if (st) return st;
-  // the counter region the decode kernels expect zero on entry
-  const int n16 = (int)(kDecodeSyncBytes / 16);
-  hipLaunchKernelGGL(clear_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0,
-                     as_stream(stream), reinterpret_cast<uint4*>(ws), n16);
-  st = check_launch("noalloc clear_kernel");
+  const int st = scratch_address(&ws);
   if (st) return st;
   return exq_moe_int4_fused_forward(problem, hidden, topk_ids, topk_weights, w13_packed,
                                     w13_scales, w2_packed, w2_scales, out, sort_order_out,

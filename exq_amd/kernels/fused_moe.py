@@ -83,9 +83,9 @@ def fused_experts(hidden_states: torch.Tensor, w13_packed: torch.Tensor,
     [0, E) are dropped).  Returns [T, H] in the activation dtype.  The call is
     stream-ordered and never synchronises with the host.  ``workspace`` (uint8,
     at least ``moe_workspace_bytes(...)``) replaces the per-stream cached one,
-    e.g. for HIP-graph capture; it must be zero-filled when first used
-    (``torch.zeros``) and must not be shared with other entry points: its first
-    bytes hold counters that every call leaves zero.
+    e.g. for HIP-graph capture; any contents will do (``torch.empty``), since
+    each call's first kernel clears the counters its first bytes hold, but it
+    must not be shared by calls that may run concurrently.
     """
     if activation != "silu":
         raise ValueError(f"unsupported activation {activation!r} (only 'silu')")

@@ -243,10 +243,9 @@ typedef struct exq_expert_bank {
 /*
  * Workspace bytes needed by the fused entry points for this problem.  The
  * first bytes of a fused-layer workspace hold the combine counters of the
- * decode kernels (T <= 64): the workspace must be zero-filled
- * before its first use, every call leaves those counters zero again, and a
- * workspace must not be shared by calls that may run concurrently or with
- * other entry points.
+ * decode kernels (T <= 64); each call's first kernel clears them, so the
+ * workspace needs no zero fill (any contents will do), but a workspace must
+ * not be shared by calls that may run concurrently.
  */
 size_t exq_moe_workspace_size(const exq_moe_problem* problem);
 
@@ -295,8 +294,9 @@ int exq_moe_mixed_forward(const exq_moe_problem* problem, const void* hidden,
  * with EXQ_ERROR_WORKSPACE_TOO_SMALL before any launch.  The call allocates
  * nothing (no hipMalloc / hipFree).  Every call on one GPU shares that GPU's
  * scratch, so calls that may overlap on one GPU (other streams, other
- * threads) race: serialise them.  Each call first clears the part of the
- * scratch that must start at zero.  Same arguments and results otherwise.
+ * threads) race: serialise them.  Nothing in the scratch needs to start at
+ * zero (the layer's first kernel clears its counters).  Same arguments and
+ * results otherwise.
  */
 #define EXQ_NOALLOC_SCRATCH_BYTES (64u << 20)
 int exq_moe_int4_fused_forward_noalloc(const exq_moe_problem* problem, const void* hidden,
