@@ -8,23 +8,29 @@ banks).  One step = one decode step through the 48 layers at batch T (16 by
 default), replayed from a HIP graph (how a serving loop issues decode
 steps); inputs are resident in HBM before the timed region.
 
-Printed: one JSON line with µs per MoE layer (value), tokens/s, the achieved
-HBM bandwidth on activated-expert weight bytes, the roofline of the dominant
-kernel (the gate/up INT4 GEMM + SiLU decode kernel, timed with HIP events
-recorded on its stream around it), the decode-batch sweep (1, 4, 16, 64) and
-the reference's CPU path timed on this host.
+Printed: one JSON line with µs per MoE layer (value: the P50 over the timed
+steps of each step's µs/layer, with P5 / P95 and the mean beside it),
+tokens/s, the achieved HBM bandwidth on activated-expert weight bytes, the
+roofline of the dominant kernel (the gate/up INT4 GEMM + SiLU decode kernel,
+timed with HIP events recorded on its stream around it, over >= 300 layer
+calls), the OLMoE T=16 line (`north_star`: BASELINE.json configs[0], the
+target configuration, with its own kernel roofline), the decode-batch sweep
+(1, 4, 16, 64), the other configurations (P50 / P5 / P95 over >= 300 layer
+calls each) and the reference's CPU path timed on this host at every
+configuration, both variants (`cpu_baseline.configs`).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--batch 16]
-                    [--sweep 1,4,16,64] [--layers 48] [--no-cpu]
+                    [--sweep 1,4,16,64] [--layers 48] [--no-cpu] [--no-configs]
 
-Counter runs (HBM traffic of the dominant kernel, rocprofv3 --pmc):
+Counter runs (HBM traffic of the dominant kernel, rocprofv3 --pmc), one per
+counter and configuration:
 
     rocprofv3 --pmc FETCH_SIZE --output-format csv -d DIR -o fetch -- \
-        python3 bench.py --pmc-run
+        python3 bench.py --pmc-run [--config olmoe --layers 3] [--batch T]
     python3 bench.py --pmc-summary DIR/.../fetch_counter_collection.csv
 
 --pmc-run first copies a 256 MiB buffer (the calibration: a plain copy of
-known size) and then runs the 48 layers once at the bench batch, eagerly.
+known size) and then runs the layers once at the bench batch, eagerly.
 """
 from __future__ import annotations
 
@@ -53,7 +59,12 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
-    ap.add_argument("--cpu-reps", type=int, default=10)
+    ap.add_argument("--cpu-reps", type=int, default=20,
+                    help="CPU baseline reps per variant and configuration (calls under 1 s)")
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="seconds per variant and configuration for calls over 1 s (>= 3 reps)")
+    ap.add_argument("--config", type=str, default="qwen3",
+                    help="with --pmc-run: the configuration of the eager pass (qwen3, olmoe)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE.json configurations")
     ap.add_argument("--pmc-run", action="store_true",
@@ -68,7 +79,7 @@ def parse_args():
 
 
 CALIB_BYTES = 256 << 20
-PMC_SUMMARY = os.path.join(ROOT, "profiles", "qwen3_t16_gateup_pmc.md")
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "decode_gateup_traffic_pmc.md")
 
 
 def pmc_summary(path):
@@ -86,13 +97,15 @@ def pmc_summary(path):
         print(f"{len(v):6d}  {ctr:12s} mean {sum(v) / len(v):14.1f}  {name[:110]}")
 
 
-def traffic_from_profile():
-    """HBM bytes per launch of the gate/up decode kernel from the committed
-    counter summary (a line `traffic_bytes_per_launch: N`), or None."""
+def traffic_from_profile(config="qwen3", T=16):
+    """HBM bytes per launch of the gate/up decode kernel at (config, T) from
+    the committed counter summary (lines `traffic_bytes_per_launch[qwen3,T=16]:
+    N`), or None when no counter run covers that configuration."""
+    key = f"traffic_bytes_per_launch[{config},T={T}]:"
     try:
         with open(PMC_SUMMARY) as f:
             for line in f:
-                if line.strip().startswith("traffic_bytes_per_launch:"):
+                if line.strip().startswith(key):
                     return int(float(line.split(":", 1)[1]))
     except (OSError, ValueError):
         return None
@@ -156,8 +169,15 @@ def run_step(stack, b):
         fused_experts(b.x, p13, s13, p2, s2, b.wts[l], b.ids[l], out=b.out, workspace=b.ws)
 
 
+def pct(v, q):
+    """q-th percentile (nearest rank) of the values v."""
+    v = sorted(v)
+    return v[min(len(v) - 1, max(0, int(round(q / 100.0 * (len(v) - 1)))))]
+
+
 def time_steps(stack, b, steps, warmup, use_graph):
-    """Returns (ms per step, host wall ms per step)."""
+    """Returns (ms per step over the bracketed K steps, host wall ms per step,
+    list of per-step ms from events recorded between the steps)."""
     import torch
     if use_graph:
         s = torch.cuda.Stream()
@@ -175,54 +195,63 @@ def time_steps(stack, b, steps, warmup, use_graph):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(steps):
+    evs[0].record()
+    for i in range(steps):
         fn()
-    ev1.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    return ev0.elapsed_time(ev1) / steps, wall
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    return evs[0].elapsed_time(evs[-1]) / steps, wall, per
 
 
-def stage_times(stack, b, reps=3):
-    """Per-kernel durations (µs) of every layer call (eager launches): the
-    decode kernels are launched with hipExtLaunchKernelGGL start / stop
-    events on the call's stream, so events 0 -> 1 time the gate/up kernel and
-    2 -> 3 the down kernel exactly."""
+def stage_times(layers, b, reps=7):
+    """Per-kernel durations (µs) of every layer call (eager launches, `reps`
+    passes over the layers): the decode kernels are launched with
+    hipExtLaunchKernelGGL start / stop events on the call's stream, so events
+    0 -> 1 time the gate/up kernel and 2 -> 3 the down kernel exactly.  Mean
+    and P5 / P50 / P95 over all calls."""
     import torch
     from exq_amd import _lib
+    from exq_amd.kernels import fused_experts
     L = _lib.lib()
-    n = len(stack.layers)
+    n = len(layers)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n * reps)]
     for row in evs:  # torch creates the HIP event on first record
         for e in row:
             e.record()
-    run_step(stack, b)
+    for l, (p13, s13, p2, s2) in enumerate(layers):
+        fused_experts(b.x, p13, s13, p2, s2, b.wts[l], b.ids[l], out=b.out, workspace=b.ws)
     torch.cuda.synchronize()
     i = 0
-    from exq_amd.kernels import fused_experts
-    for _ in range(reps):
-        for l, (p13, s13, p2, s2) in enumerate(stack.layers):
-            arr = (ctypes.c_void_p * 4)(*[e.cuda_event for e in evs[i]])
-            _lib.check(L.exq_set_stage_events(arr, 4), "exq_set_stage_events")
-            fused_experts(b.x, p13, s13, p2, s2, b.wts[l], b.ids[l], out=b.out, workspace=b.ws)
-            i += 1
+    try:
+        for _ in range(reps):
+            for l, (p13, s13, p2, s2) in enumerate(layers):
+                arr = (ctypes.c_void_p * 4)(*[e.cuda_event for e in evs[i]])
+                _lib.check(L.exq_set_stage_events(arr, 4), "exq_set_stage_events")
+                fused_experts(b.x, p13, s13, p2, s2, b.wts[l], b.ids[l], out=b.out,
+                              workspace=b.ws)
+                i += 1
+    finally:
+        _lib.check(L.exq_set_stage_events(None, 0), "exq_set_stage_events")
     torch.cuda.synchronize()
-    gateup = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
-    down = [e[2].elapsed_time(e[3]) * 1e3 for e in evs]
-    layer = [e[0].elapsed_time(e[3]) * 1e3 for e in evs]
-    mean = lambda v: sum(v) / len(v)  # noqa: E731
-    return {"gateup_us": mean(gateup), "down_us": mean(down), "layer_us": mean(layer)}
+    out = {"calls": len(evs)}
+    for name, (a, z) in (("gateup", (0, 1)), ("down", (2, 3)), ("layer", (0, 3))):
+        v = [e[a].elapsed_time(e[z]) * 1e3 for e in evs]
+        out[f"{name}_us"] = sum(v) / len(v)
+        out[f"{name}_p5_us"], out[f"{name}_p50_us"], out[f"{name}_p95_us"] = (
+            pct(v, 5), pct(v, 50), pct(v, 95))
+    return out
 
 
 MFMA_PEAK_BF16_TFLOPS = 2500.0
 
 
-def _graph_time(fn, reps, warmup=3):
-    """Mean ms per call of `fn` replayed from a HIP graph."""
+def _graph_times(fn, reps, warmup=3):
+    """Per-replay ms of `fn` captured once in a HIP graph and replayed `reps`
+    times (events recorded between the replays)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -236,14 +265,19 @@ def _graph_time(fn, reps, warmup=3):
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    evs[0].record()
+    for i in range(reps):
         g.replay()
-    e1.record()
+        evs[i + 1].record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / reps
+    return [evs[i].elapsed_time(evs[i + 1]) for i in range(reps)]
+
+
+def _graph_time(fn, reps, warmup=3):
+    """Mean ms per call of `fn` replayed from a HIP graph."""
+    v = _graph_times(fn, reps, warmup)
+    return sum(v) / len(v)
 
 
 def _deepseek_bank(cfg, layer, dev):
@@ -303,35 +337,58 @@ def prefill_rows(calls, reps):
     return rows
 
 
-def measure_configs(dev, reps):
+class _Calls:
+    """Inputs of one decode batch over a rotation of layers (stage_times'
+    batch interface)."""
+
+    def __init__(self, x, ids, wts, out, ws):
+        self.x, self.ids, self.wts, self.out, self.ws = x, ids, wts, out, ws
+
+
+def measure_configs(dev, reps, cpu=None):
     """The other BASELINE.json configurations: decode µs/layer and achieved GB/s
     on activated-expert bytes (weights + scales; shared experts included) over
-    distinct seeded layers replayed from a HIP graph, and prefill TFLOP/s."""
+    distinct seeded layers replayed from a HIP graph, and prefill TFLOP/s.
+
+    Returns (rows, north_star, cpu_rows): north_star is the OLMoE T=16 line
+    (the target configuration) with its own stage
+    events and roofline; cpu_rows (when ``cpu`` holds the CPU settings) the
+    reference CPU path timed on layer 0 of each configuration, same inputs."""
+    import json as _json
+    import tempfile
     import numpy as np
     import torch
     from exq_amd import synth
     from exq_amd.kernels import (MixedExpertBank, fused_experts, fused_experts_mixed,
-                                 pack_experts_int4)
+                                 load_exq_artifact, pack_experts_int4)
     from exq_amd.kernels.fused_moe import moe_workspace_bytes
-    rows = []
+    rows, cpu_rows = [], []
+    north_star = None
 
     def ws_for(cfg, T):  # explicit workspace: nothing allocates inside graph capture
-        return torch.zeros(moe_workspace_bytes(T, cfg.hidden, cfg.inter, cfg.n_experts,
+        return torch.empty(moe_workspace_bytes(T, cfg.hidden, cfg.inter, cfg.n_experts,
                                                cfg.top_k, cfg.n_shared), dtype=torch.uint8,
                            device=dev)
 
     def decode_row(name, cfg, T, calls, bytes_per_call, n_layers):
         # One graph holds at least 48 layer calls (the rotation repeated), as a
-        # model's decode step does, so one graph launch is not charged to a few layers.
+        # model's decode step does, so one graph launch is not charged to a few
+        # layers; µs/layer of each replay, P50 (P5 / P95 beside it) over `reps`
+        # replays (>= 300 layer calls).
         seq = calls * max(1, -(-48 // len(calls)))
-        ms = _graph_time(lambda: [c() for c in seq], reps)
-        us = ms * 1e3 / len(seq)
+        n_rep = max(reps, -(-300 // len(seq)))
+        per = [ms * 1e3 / len(seq) for ms in _graph_times(lambda: [c() for c in seq], n_rep)]
+        us = pct(per, 50)
         gbps = bytes_per_call / (us * 1e-6) / 1e9
         rows.append({"config": name, "batch": T, "layers_rotated": n_layers,
-                     "calls_per_graph": len(seq),
-                     "us_per_layer": round(us, 2), "tokens_per_s": round(T / (us * 1e-6)),
+                     "calls_per_graph": len(seq), "layer_calls_timed": len(seq) * n_rep,
+                     "us_per_layer": round(us, 2), "p5_us": round(pct(per, 5), 2),
+                     "p95_us": round(pct(per, 95), 2),
+                     "mean_us": round(sum(per) / len(per), 2),
+                     "tokens_per_s": round(T / (us * 1e-6)),
                      "achieved_GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4)})
-        log(f"config {name} T={T}: {us:.2f} us/layer, {gbps:.0f} GB/s")
+        log(f"config {name} T={T}: {us:.2f} us/layer P50, {gbps:.0f} GB/s")
+        return rows[-1]
 
     def routing_for(cfg, T, layer):
         ids, w = synth.routing(cfg, T, layer)
@@ -347,44 +404,93 @@ def measure_configs(dev, reps):
             del w13, w2
         return out
 
+    def cpu_int4(name, T, x, layer, tid, tw):
+        if cpu is not None:
+            from oracle.cpu_baseline import int4_deq
+            cpu_rows.append(cpu_config_row(name, T, x, int4_deq(*layer), (), tid, tw, cpu))
+
+    def cpu_bank(name, T, x, bank, tid, tw):
+        if cpu is not None:
+            from oracle.cpu_baseline import bank_deq
+            tensors = {n: getattr(bank, n) for n in (
+                "bf16_w13", "bf16_w2", "int8_w13", "int8_w13_scales", "int8_w2",
+                "int8_w2_scales", "int4_w13", "int4_w13_scales", "int4_w2", "int4_w2_scales")}
+            tensors["n_experts"] = bank.n_experts
+            routed, shared = bank_deq(bank.tier.tolist(), bank.index.tolist(), tensors,
+                                      tid.reshape(-1).tolist())
+            cpu_rows.append(cpu_config_row(name, T, x, routed, shared, tid, tw, cpu))
+
     # OLMoE single INT4 layer; 3 distinct layers so the 198 MiB
     # bank does not sit in the 256 MB Infinity Cache between calls
     cfg = synth.CONFIGS["olmoe"]
     layers = int4_layers(cfg, 3)
     eb = synth.int4_expert_bytes(cfg.hidden, cfg.inter, cfg.group_size)
+    w13_bytes = 2 * cfg.inter * cfg.hidden // 2 + 2 * cfg.inter * (cfg.hidden // cfg.group_size) * 2
     for T in (1, 16, 64):
         x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 77 + T)).to(torch.bfloat16).to(dev)
         ws = ws_for(cfg, T)
-        calls, nbytes = [], 0
+        calls, nbytes, active, rts = [], 0, [], []
         for l, (p13, s13, p2, s2) in enumerate(layers):
             tid, tw, ids = routing_for(cfg, T, l)
-            nbytes += np.unique(ids).size * eb
+            rts.append((tid, tw))
+            active.append(np.unique(ids).size)
+            nbytes += active[-1] * eb
             calls.append(lambda p13=p13, s13=s13, p2=p2, s2=s2, tw=tw, tid=tid, x=x, ws=ws:
                          fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws))
-        decode_row("olmoe", cfg, T, calls, nbytes / len(layers), len(layers))
+        row = decode_row("olmoe", cfg, T, calls, nbytes / len(layers), len(layers))
+        if T == 16:
+            out = torch.empty(T, cfg.hidden, dtype=torch.bfloat16, device=dev)
+            b = _Calls(x, [r[0] for r in rts], [r[1] for r in rts], out, ws)
+            st = stage_times(layers, b, reps=max(3, -(-300 // len(layers))))
+            kb = w13_bytes * sum(active) / len(active)
+            kg = kb / (st["gateup_us"] * 1e-6) / 1e9
+            north_star = dict(row)
+            north_star.update({
+                "active_experts_mean": round(sum(active) / len(active), 2),
+                "roofline": {"bound": "hbm",
+                             "kernel": "moe_decode_kernel<bf16, gate/up, NT=1, INT4 LDS path>",
+                             "achieved": round(kg, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                             "frac": round(kg / HBM_PEAK_GBPS, 4),
+                             "traffic": traffic_from_profile("olmoe", T),
+                             "bytes_per_launch": round(kb), "launch_us": round(st["gateup_us"], 3)},
+                "stages_us": {k: round(v, 3) for k, v in st.items()}})
+            log(f"north star olmoe T=16: {row['us_per_layer']} us/layer, gate/up {kg:.0f} GB/s")
+        cpu_int4("olmoe", T, x, layers[0], rts[0][0], rts[0][1])
     del layers
     torch.cuda.empty_cache()
 
-    # Mixed-precision OLMoE stack: 16 layers, BF16/INT8/INT4 per layer
+    # Mixed-precision OLMoE stack: 16 layers, BF16/INT8/INT4 per
+    # expert from the quant-plan artifact (tiers ranked by the router's own
+    # Zipf frequencies), read back with the artifact reader as a deployment would
     cfg = synth.CONFIGS["mixed_olmoe"]
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "mixed_olmoe_plan.json")
+        with open(path, "w", encoding="utf-8") as f:
+            _json.dump(synth.plan_artifact(cfg), f)
+        plan = load_exq_artifact(path, device="cpu")
     banks = []
     for l in range(cfg.n_layers):
         w13, w2 = synth.expert_weights_gpu(cfg.n_experts, cfg.inter, cfg.hidden,
                                            synth.seed_for(cfg, l), dev)
-        banks.append(MixedExpertBank.from_weights(w13, w2,
-                                                  synth.mixed_tiers(cfg.n_experts,
-                                                                    synth.seed_for(cfg, l))))
+        banks.append(MixedExpertBank.from_weights(w13, w2, plan.tiers[l].tolist()))
         del w13, w2
     T = 32
     x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 99)).to(torch.bfloat16).to(dev)
     ws = ws_for(cfg, T)
-    calls, nbytes = [], 0
+    calls, nbytes, share, rts = [], 0, [], []
     for l, bank in enumerate(banks):
         tid, tw, ids = routing_for(cfg, T, l)
-        nbytes += sum(bank.stored_bytes(int(e)) for e in np.unique(ids))
+        rts.append((tid, tw))
+        used = np.unique(ids)
+        b = [bank.stored_bytes(int(e)) for e in used]
+        nbytes += sum(b)
+        share.append(sum(v for e, v in zip(used, b) if int(bank.tier[int(e)]) == 0) / sum(b))
         calls.append(lambda bank=bank, tw=tw, tid=tid: fused_experts_mixed(x, bank, tw, tid,
                                                                          workspace=ws))
-    decode_row("mixed_olmoe", cfg, T, calls, nbytes / len(banks), len(banks))
+    row = decode_row("mixed_olmoe", cfg, T, calls, nbytes / len(banks), len(banks))
+    row["plan"] = "artifact (router-ranked: top 10% BF16, next 20% INT8, rest INT4)"
+    row["bf16_byte_share"] = round(sum(share) / len(share), 4)
+    cpu_bank("mixed_olmoe", T, x, banks[0], rts[0][0], rts[0][1])
     del banks
     torch.cuda.empty_cache()
 
@@ -404,13 +510,16 @@ def measure_configs(dev, reps):
     for T in (1, 16, 64):
         x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 55 + T)).to(torch.bfloat16).to(dev)
         ws = ws_for(cfg, T)
-        calls, nbytes = [], 0
+        calls, nbytes, rts = [], 0, []
         for l, bank in enumerate(banks):
             tid, tw, ids = routing_for(cfg, T, l)
+            rts.append((tid, tw))
             nbytes += np.unique(ids).size * eb + shared_bytes
             calls.append(lambda bank=bank, tw=tw, tid=tid, x=x, ws=ws:
                          fused_experts_mixed(x, bank, tw, tid, workspace=ws))
         decode_row("deepseek_v2_lite", cfg, T, calls, nbytes / len(banks), len(banks))
+        if T != 16:
+            cpu_bank("deepseek_v2_lite", T, x, banks[0], rts[0][0], rts[0][1])
     rows += prefill_rows([_prefill_call(dev, "deepseek_v2_lite", banks[0])], max(3, reps // 10))
     del banks
     torch.cuda.empty_cache()
@@ -422,13 +531,15 @@ def measure_configs(dev, reps):
     for T in (1, 16, 64):
         x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 11 + T)).to(torch.bfloat16).to(dev)
         ws = ws_for(cfg, T)
-        calls, nbytes = [], 0
+        calls, nbytes, rts = [], 0, []
         for l, (p13, s13, p2, s2) in enumerate(layers):
             tid, tw, ids = routing_for(cfg, T, l)
+            rts.append((tid, tw))
             nbytes += np.unique(ids).size * eb
             calls.append(lambda p13=p13, s13=s13, p2=p2, s2=s2, tw=tw, tid=tid, x=x, ws=ws:
                          fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws))
         decode_row("mixtral", cfg, T, calls, nbytes / len(layers), len(layers))
+        cpu_int4("mixtral", T, x, layers[0], rts[0][0], rts[0][1])
     rows += prefill_rows([_prefill_call(dev, "mixtral", layers[0])], max(3, reps // 10))
     del layers
     torch.cuda.empty_cache()
@@ -445,36 +556,61 @@ def measure_configs(dev, reps):
         rows.append({"config": "router_qwen3", "batch": T, "experts": cfg.n_experts,
                      "top_k": cfg.top_k, "calls_per_graph": n, "us_per_call": round(ms * 1e3, 2)})
         log(f"config router qwen3 T={T}: {ms * 1e3:.2f} us")
-    return rows
+    return rows, north_star, cpu_rows
 
 
-def cpu_baseline(stack, b, reps):
-    """The reference's PyTorch CPU path (oracle/cpu_baseline.py) on this host."""
-    import torch
-    from oracle.cpu_baseline import time_cpu_layer
-    p13, s13, p2, s2 = stack.layers[0]
-    # the box's CPU share (OMP_NUM_THREADS), not every core the host reports
-    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    r = time_cpu_layer(b.x, p13, s13, p2, s2, b.ids[0], b.wts[0], "dequant_per_call",
-                       reps=reps, warmup=1, threads=threads)
-    r2 = time_cpu_layer(b.x, p13, s13, p2, s2, b.ids[0], b.wts[0], "predequantized",
-                        reps=reps, warmup=1, threads=threads)
-    model = ""
+def cpu_model():
+    """lscpu-style model name of the host CPU."""
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": round(r["p50_us"], 1), "unit": "us/layer", "cores": threads,
+    return platform.processor() or "unknown"
+
+
+def cpu_threads():
+    # the box's CPU share (OMP_NUM_THREADS), not every core the host reports
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+
+
+def cpu_config_row(name, T, x, routed, shared, tid, tw, cpu):
+    """Both variants of the reference CPU path on one configuration's layer:
+    dequantise per call (reference-faithful) and pre-dequantised."""
+    from oracle.cpu_baseline import time_cpu_experts
+    row = {"config": name, "batch": T}
+    for variant in ("dequant_per_call", "predequantized"):
+        r = time_cpu_experts(x, routed, tid, tw, shared, variant, reps=cpu["reps"], warmup=1,
+                             threads=cpu["threads"], budget_s=cpu["budget_s"])
+        row[variant] = {"p50_us": round(r["p50_us"], 1), "p5_us": round(r["p5_us"], 1),
+                        "p95_us": round(r["p95_us"], 1), "reps": r["reps"],
+                        "tokens_per_s": round(T / (r["p50_us"] * 1e-6), 1)}
+    log(f"cpu {name} T={T}: {row['dequant_per_call']['p50_us'] / 1e3:.1f} ms "
+        f"(predequantized {row['predequantized']['p50_us'] / 1e3:.1f} ms)")
+    return row
+
+
+def cpu_int4_bank(stack):
+    from oracle.cpu_baseline import int4_deq
+    return int4_deq(*stack.layers[0])
+
+
+def cpu_baseline(deq, b, cpu):
+    """The reference's PyTorch CPU path (oracle/cpu_baseline.py) on this host:
+    the headline sample, Qwen3 layer 0 (dequantisers ``deq``) at the bench
+    batch."""
+    import torch
+    row = cpu_config_row("qwen3", b.T, b.x, deq, (), b.ids[0], b.wts[0], cpu)
+    d, p = row["dequant_per_call"], row["predequantized"]
+    return {"value": d["p50_us"], "unit": "us/layer", "cores": cpu["threads"],
             "kind": "port",
-            "sample": f"qwen3 layer 0, T={b.T}, {reps} reps P50, dequant per call "
+            "sample": f"qwen3 layer 0, T={b.T}, {d['reps']} reps P50, dequant per call "
                       f"(pytorch_moe_reference loop, torch {torch.__version__} CPU fp32, "
-                      f"{threads} threads, {model or platform.processor()})",
-            "p5_us": round(r["p5_us"], 1), "p95_us": round(r["p95_us"], 1),
-            "predequantized_p50_us": round(r2["p50_us"], 1)}
+                      f"{cpu['threads']} threads, {cpu_model()})",
+            "p5_us": d["p5_us"], "p95_us": d["p95_us"],
+            "predequantized_p50_us": p["p50_us"], "cpu_model": cpu_model()}
 
 
 def main():
@@ -494,7 +630,7 @@ def main():
         print("bench.py needs a HIP GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda", 0)
-    cfg = synth.CONFIGS["qwen3"]
+    cfg = synth.CONFIGS["qwen3" if not args.pmc_run else args.config]
     if args.prefill_only:  # the MFMA-path configurations alone (profiles, counter runs)
         rows = []
         for name in ("deepseek_v2_lite", "mixtral"):
@@ -530,12 +666,14 @@ def main():
         log(f"one eager pass of {args.layers} layers at T={args.batch}; activated experts "
             f"per layer {sum(b.active) / len(b.active):.2f}")
         return
-    ms, wall = time_steps(stack, b, args.steps, args.warmup, use_graph)
-    us_layer = ms * 1e3 / args.layers
-    gbps = b.bytes / (ms * 1e-3) / 1e9
-    log(f"T={args.batch}: {ms:.3f} ms/step, {us_layer:.2f} us/layer, {gbps:.0f} GB/s "
+    ms, wall, per = time_steps(stack, b, args.steps, args.warmup, use_graph)
+    per_layer = [m * 1e3 / args.layers for m in per]  # µs/layer of each step
+    us_layer = pct(per_layer, 50)
+    gbps = b.bytes / (us_layer * args.layers * 1e-6) / 1e9
+    log(f"T={args.batch}: {ms:.3f} ms/step mean, {us_layer:.2f} us/layer P50 "
+        f"(P5 {pct(per_layer, 5):.2f}, P95 {pct(per_layer, 95):.2f}), {gbps:.0f} GB/s "
         f"(host wall {wall:.3f} ms/step)")
-    st = stage_times(stack, b)
+    st = stage_times(stack.layers, b, reps=max(1, -(-300 // args.layers)))
     log(f"stage events: {st}")
     # Dominant kernel: the gate/up decode kernel (events 0 -> 1 time it on the
     # call's stream); its algorithmic bytes are the activated experts'
@@ -543,30 +681,47 @@ def main():
     kern_us = st["gateup_us"]
     kern_bytes = stack.w13_bytes * sum(b.active) / len(b.active)
     kern_gbps = kern_bytes / (kern_us * 1e-6) / 1e9
-    traffic = traffic_from_profile()
+    traffic = traffic_from_profile("qwen3", args.batch)
 
     sweep = []
     for T in [int(v) for v in args.sweep.split(",") if v.strip()]:
         bb = b if T == args.batch else Batch(stack, T, dev)
-        m, _ = time_steps(stack, bb, max(10, args.steps // 2), args.warmup, use_graph)
-        ul = m * 1e3 / args.layers
-        g = bb.bytes / (m * 1e-3) / 1e9
-        sweep.append({"batch": T, "us_per_layer": round(ul, 2), "tokens_per_s": round(T / (ul * 1e-6)),
+        _, _, pr = time_steps(stack, bb, max(10, args.steps // 2), args.warmup, use_graph)
+        pl = [m * 1e3 / args.layers for m in pr]
+        ul = pct(pl, 50)
+        g = bb.bytes / (ul * args.layers * 1e-6) / 1e9
+        sweep.append({"batch": T, "us_per_layer": round(ul, 2), "p5_us": round(pct(pl, 5), 2),
+                      "p95_us": round(pct(pl, 95), 2), "layer_calls_timed": len(pl) * args.layers,
+                      "tokens_per_s": round(T / (ul * 1e-6)),
                       "active_experts_mean": round(sum(bb.active) / len(bb.active), 2),
                       "achieved_GBps": round(g, 1), "frac_of_peak": round(g / HBM_PEAK_GBPS, 4)})
-        log(f"sweep T={T}: {ul:.2f} us/layer, {g:.0f} GB/s")
+        log(f"sweep T={T}: {ul:.2f} us/layer P50, {g:.0f} GB/s")
         if bb is not b:
             del bb
-    configs = None
+    cpu_set = None if args.no_cpu else {"threads": cpu_threads(), "reps": args.cpu_reps,
+                                        "budget_s": args.cpu_budget}
+    cpu, cpu_rows = None, []
+    if cpu_set is not None:
+        t1 = time.time()
+        deq = cpu_int4_bank(stack)
+        cpu = cpu_baseline(deq, b, cpu_set)
+        for T in [int(v) for v in args.sweep.split(",") if v.strip()]:
+            if T == args.batch:
+                continue
+            bb = Batch(stack, T, dev)
+            cpu_rows.append(cpu_config_row("qwen3", T, bb.x, deq, (), bb.ids[0], bb.wts[0],
+                                           cpu_set))
+            del bb
+        del deq
+        log(f"cpu baseline {cpu['value']} us/layer in {time.time() - t1:.1f}s")
+    configs, north_star = None, None
     if not args.no_configs:
         t1 = time.time()
-        configs = measure_configs(dev, max(20, args.steps))
+        configs, north_star, more = measure_configs(dev, max(20, args.steps), cpu_set)
+        cpu_rows += more
         log(f"configs measured in {time.time() - t1:.1f}s")
-    cpu = None
-    if not args.no_cpu:
-        t1 = time.time()
-        cpu = cpu_baseline(stack, b, args.cpu_reps)
-        log(f"cpu baseline {cpu['value']} us/layer in {time.time() - t1:.1f}s")
+    if cpu is not None:
+        cpu["configs"] = cpu_rows
 
     out = {
         "metric": METRIC,
@@ -588,6 +743,11 @@ def main():
                    "batch": args.batch, "layers": args.layers, "hidden": cfg.hidden,
                    "inter": cfg.inter, "experts": cfg.n_experts, "top_k": cfg.top_k,
                    "launch": "hip-graph replay" if use_graph else "eager"},
+        "statistic": f"P50 of per-step µs/layer over {args.steps} steps "
+                     f"({args.steps * args.layers} layer calls)",
+        "p5_us": round(pct(per_layer, 5), 3),
+        "p95_us": round(pct(per_layer, 95), 3),
+        "mean_us": round(ms * 1e3 / args.layers, 3),
         "tokens_per_s": round(args.batch / (us_layer * 1e-6)),
         "achieved_GBps": round(gbps, 1),
         "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
@@ -597,6 +757,7 @@ def main():
                      "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": round(kern_bytes), "launch_us": round(kern_us, 3)},
         "stages_us": {k: round(v, 3) for k, v in st.items()},
+        "north_star": north_star,
         "sweep": sweep,
         "configs": configs,
         "cpu_baseline": cpu,

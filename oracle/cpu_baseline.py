@@ -12,12 +12,15 @@ Steps (the reference's CPU path, composed into a full layer):
   5. the top-k weighted sum.
 Variant ``"dequant_per_call"`` dequantises the routed experts inside every
 call (reference-faithful); ``"predequantized"`` keeps fp32 weights and times
-the matmuls only.
+the matmuls only.  Mixed-precision banks dequantise each expert by its tier
+(INT4 as above, INT8 per-row fp16 scale, BF16 widened); always-on shared
+experts are added with weight 1, as the GPU path does.
 
-pinned by: tests/test_oracle_cpu_baseline.py -- ``dequant_int4_torch`` equals
-``oracle.quant.dequant_int4`` bit for bit, and ``moe_layer_loop`` equals
+pinned by: tests/test_oracle_cpu_baseline.py -- ``dequant_int4_torch`` and
+``dequant_int8_torch`` equal ``oracle.quant.dequant_int4`` / ``dequant_int8``
+bit for bit, and ``moe_layer_loop`` (with and without shared experts) equals
 ``oracle.moe.moe_layer`` (float64) to 1e-5 relative L2, while a dropped top-k
-term misses it by more than 1e-2.
+term or a dropped shared expert misses it by more than 1e-2.
 """
 from __future__ import annotations
 
@@ -42,45 +45,70 @@ def dequant_int4_torch(packed: torch.Tensor, scales: torch.Tensor) -> torch.Tens
     return w
 
 
+def dequant_int8_torch(q: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    """[..., N, K] i8 + [..., N] f16 per-row scales -> fp32 [..., N, K]."""
+    return q.float() * scales.float().unsqueeze(-1)
+
+
 def moe_layer_loop(x: torch.Tensor, w13: dict, w2: dict, ids: torch.Tensor,
-                   wts: torch.Tensor) -> torch.Tensor:
-    """pytorch_moe_reference's per-(token, k) loop, extended to the full layer."""
+                   wts: torch.Tensor, shared: tuple = ()) -> torch.Tensor:
+    """pytorch_moe_reference's per-(token, k) loop, extended to the full layer;
+    ``shared`` holds (w13, w2) of always-on experts, added with weight 1."""
     T, k = ids.shape
     out = torch.zeros(T, x.shape[1], dtype=torch.float32)
     for t in range(T):
         for j in range(k):
             e = int(ids[t, j])
+            if e < 0 or e not in w13:  # dropped slot
+                continue
             gu = w13[e] @ x[t]
             I = gu.shape[0] // 2
             mid = torch.nn.functional.silu(gu[:I]) * gu[I:]
             out[t] += float(wts[t, j]) * (w2[e] @ mid)
+        for s13, s2 in shared:
+            gu = s13 @ x[t]
+            I = gu.shape[0] // 2
+            out[t] += s2 @ (torch.nn.functional.silu(gu[:I]) * gu[I:])
     return out
 
 
-def time_cpu_layer(x, p13, s13, p2, s2, ids, wts, variant: str = "dequant_per_call",
-                   reps: int = 20, warmup: int = 2, threads: int | None = None) -> dict:
-    """Time one MoE layer on the host CPU; returns P5/P50/P95 in microseconds."""
+def time_cpu_experts(x, deq: dict, ids, wts, shared_deq=(), variant: str = "dequant_per_call",
+                     reps: int = 20, warmup: int = 1, threads: int | None = None,
+                     budget_s: float | None = None) -> dict:
+    """Time one MoE layer whose routed expert e dequantises with ``deq[e]()``
+    (returning fp32 (w13, w2) from host copies of the stored tensors) and whose
+    shared experts with ``shared_deq``; P5/P50/P95 in microseconds.
+
+    With ``budget_s`` the first warm-up call sizes the run: 20 reps (``reps``)
+    when a call takes under a second, otherwise as many as fit the budget, at
+    least 3."""
     threads = threads or os.cpu_count() or 1
     torch.set_num_threads(threads)
     x = x.float().cpu()
     ids = ids.cpu()
     wts = wts.float().cpu()
-    used = sorted(set(int(v) for v in ids.reshape(-1).tolist()))
-    p13, s13, p2, s2 = (t.cpu() for t in (p13, s13, p2, s2))
+    used = sorted(set(int(v) for v in ids.reshape(-1).tolist()) & set(deq))
 
-    def deq():
-        return ({e: dequant_int4_torch(p13[e], s13[e]) for e in used},
-                {e: dequant_int4_torch(p2[e], s2[e]) for e in used})
+    def dequant_all():
+        w13, w2 = {}, {}
+        for e in used:
+            w13[e], w2[e] = deq[e]()
+        return w13, w2, tuple(f() for f in shared_deq)
 
-    pre = deq() if variant == "predequantized" else None
+    pre = dequant_all() if variant == "predequantized" else None
 
     def run():
-        a, b = pre if pre is not None else deq()
-        return moe_layer_loop(x, a, b, ids, wts)
+        a, b, sh = pre if pre is not None else dequant_all()
+        return moe_layer_loop(x, a, b, ids, wts, sh)
 
     with torch.no_grad():
-        for _ in range(warmup):
+        first = None
+        for _ in range(max(warmup, 1 if budget_s else 0)):
+            t0 = time.perf_counter()
             run()
+            first = time.perf_counter() - t0
+        if budget_s and first is not None and first >= 1.0:
+            reps = max(3, min(reps, int(budget_s / first)))
         times = []
         for _ in range(reps):
             t0 = time.perf_counter()
@@ -91,3 +119,48 @@ def time_cpu_layer(x, p13, s13, p2, s2, ids, wts, variant: str = "dequant_per_ca
     return {"variant": variant, "threads": threads, "reps": n,
             "p50_us": times[n // 2], "p5_us": times[int(0.05 * (n - 1))],
             "p95_us": times[int(0.95 * (n - 1))], "mean_us": statistics.mean(times)}
+
+
+def int4_deq(p13, s13, p2, s2) -> dict:
+    """Per-expert INT4 dequantisers over host copies of a packed bank."""
+    p13, s13, p2, s2 = (t.cpu() for t in (p13, s13, p2, s2))
+    return {e: (lambda e=e: (dequant_int4_torch(p13[e], s13[e]),
+                             dequant_int4_torch(p2[e], s2[e])))
+            for e in range(p13.shape[0])}
+
+
+def bank_deq(tier, index, tensors: dict, used) -> tuple[dict, list]:
+    """Per-expert dequantisers of a mixed-precision bank (tier 0 BF16, 1 INT8,
+    2 INT4; ``index`` the row in the tier's tensors), for the routed experts in
+    ``used`` and every shared expert (ids from len(used bank) on).  Only the
+    rows that are needed are copied to the host."""
+    tier = [int(v) for v in tier]
+    index = [int(v) for v in index]
+
+    def host(name, i):
+        return tensors[name][i].cpu()
+
+    def make(e):
+        t, i = tier[e], index[e]
+        if t == 0:
+            a, b = host("bf16_w13", i), host("bf16_w2", i)
+            return lambda: (a.float(), b.float())
+        if t == 1:
+            a, sa = host("int8_w13", i), host("int8_w13_scales", i)
+            b, sb = host("int8_w2", i), host("int8_w2_scales", i)
+            return lambda: (dequant_int8_torch(a, sa), dequant_int8_torch(b, sb))
+        a, sa = host("int4_w13", i), host("int4_w13_scales", i)
+        b, sb = host("int4_w2", i), host("int4_w2_scales", i)
+        return lambda: (dequant_int4_torch(a, sa), dequant_int4_torch(b, sb))
+
+    n_routed = tensors["n_experts"]
+    routed = {e: make(e) for e in sorted(set(int(u) for u in used)) if 0 <= e < n_routed}
+    shared = [make(e) for e in range(n_routed, len(tier))]
+    return routed, shared
+
+
+def time_cpu_layer(x, p13, s13, p2, s2, ids, wts, variant: str = "dequant_per_call",
+                   reps: int = 20, warmup: int = 2, threads: int | None = None) -> dict:
+    """Time one all-INT4 MoE layer on the host CPU; P5/P50/P95 in microseconds."""
+    return time_cpu_experts(x, int4_deq(p13, s13, p2, s2), ids, wts, (), variant, reps,
+                            warmup, threads)
