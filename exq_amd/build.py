@@ -17,7 +17,7 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libexq_hip.so"
 
-SOURCES = ["elementwise.hip", "routing.hip", "pack.hip", "moe_mfma.hip", "decode.hip", "prefill.hip", "noalloc.hip"]
+SOURCES = ["elementwise.hip", "routing.hip", "pack.hip", "moe_mfma.hip", "decode.hip", "prefill.hip", "general.hip", "noalloc.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -1211,6 +1211,7 @@ int resident_work_groups(const void* kern, int threads, size_t lds, int* out) {
 bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, int64_t H,
                            int64_t I, int64_t group_size) {
   const int64_t gkb = group_size / 128;  // k-blocks per scale group: a power of two
+  if (H % 128 || I % 128 || group_size % 128) return false;
   if (!(T >= 1 && T <= 64 && T * k <= MAX_SLOTS && Ep <= kDecodeMaxBuckets && n_shared <= 64 &&
         H / 32 <= kDecodeMaxHBlocks && H % 64 == 0 && gkb >= 1 && (gkb & (gkb - 1)) == 0))
     return false;

@@ -76,6 +76,13 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
                      int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s);
 
+// INT4 grouped GEMMs for the shapes outside the tiled / grouped kernels
+// (general.hip): K % 32 == 0, a group size that is a multiple of 32 dividing
+// K, any number of weight rows.  Token groups [hdr[1], hdr[0]) (<= 64 rows),
+// n_blocks = ceil(output columns / 16).
+bool general_shape(int64_t K, int64_t group_size);
+int launch_general_gemm(int mode, bool bf, const GemmArgs& a, int64_t tg_cap, hipStream_t s);
+
 // Parameters of the routing-plan kernel (one work-group).
 struct RoutePlanParams {
   const void* ids;

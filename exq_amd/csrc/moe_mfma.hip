@@ -508,18 +508,23 @@ int validate_problem(const exq_moe_problem* p, const char* fn) {
   EXQ_REQUIRE(p->n_tokens * (p->top_k + p->n_shared) <= (1 << 24),
               "%s: T*(k+shared) = %lld exceeds 2^24 slots", fn,
               (long long)(p->n_tokens * (p->top_k + p->n_shared)));
-  EXQ_REQUIRE_SUPPORTED(p->hidden_size >= 128 && p->hidden_size % 128 == 0,
-                        "%s: hidden_size=%lld must be a positive multiple of 128", fn,
+  EXQ_REQUIRE_SUPPORTED(p->hidden_size >= 32 && p->hidden_size % 32 == 0,
+                        "%s: hidden_size=%lld must be a positive multiple of 32", fn,
                         (long long)p->hidden_size);
-  EXQ_REQUIRE_SUPPORTED(p->inter_size >= 128 && p->inter_size % 128 == 0,
-                        "%s: inter_size=%lld must be a positive multiple of 128", fn,
+  EXQ_REQUIRE_SUPPORTED(p->inter_size >= 32 && p->inter_size % 32 == 0,
+                        "%s: inter_size=%lld must be a positive multiple of 32", fn,
                         (long long)p->inter_size);
-  EXQ_REQUIRE_SUPPORTED(p->group_size >= 128 && p->group_size % 128 == 0 &&
-                            p->hidden_size % p->group_size == 0 &&
-                            p->inter_size % p->group_size == 0,
-                        "%s: group_size=%lld must be a multiple of 128 dividing H and I", fn,
+  EXQ_REQUIRE_SUPPORTED(general_shape(p->hidden_size, p->group_size) &&
+                            general_shape(p->inter_size, p->group_size),
+                        "%s: group_size=%lld must be a multiple of 32 dividing H and I", fn,
                         (long long)p->group_size);
   return EXQ_SUCCESS;
+}
+
+// Shapes the decode, tiled and grouped kernels take: H, I and the group size
+// multiples of 128.  Other all-INT4 shapes run on the general kernels.
+bool standard_shape(const exq_moe_problem* p) {
+  return p->hidden_size % 128 == 0 && p->inter_size % 128 == 0 && p->group_size % 128 == 0;
 }
 
 int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void* topk_ids,
@@ -557,8 +562,13 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   // when both projections fit them and the gathered activations are 32-bit
   // addressable; INT8 experts (and everything else) on the grouped kernel.
   const int gs = (int)p->group_size;
+  // all-INT4 layers of other shapes: routing plan + general kernels + combine
+  const bool general = !standard_shape(p);
+  EXQ_REQUIRE_SUPPORTED(!general || tier == nullptr,
+                        "%s: mixed-precision banks need H, I and group_size multiples of 128 "
+                        "(got H=%d I=%d g=%d)", fn, H, I, gs);
   const bool x32 = (int64_t)T * H * 2 <= 0x7fffffffLL;
-  const bool tile = x32 && tile_gemm_applies(2, MODE_GATEUP, 2 * I, I, H, gs) &&
+  const bool tile = !general && x32 && tile_gemm_applies(2, MODE_GATEUP, 2 * I, I, H, gs) &&
                     tile_gemm_applies(2, MODE_DOWN, H, I, I, gs) &&
                     tile_rowsum_floats(L.n, I) * 4 <= 0x7fffffffLL;
   const bool tile_bf = tier != nullptr && x32 &&
@@ -576,8 +586,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   struct HookReset {  // the hook is consumed by this call, whatever happens
     ~HookReset() { g_stage_events_set = false; }
   } hook_reset;
-  const bool decode =
-      decode_path_supported(T, k, Ep, p->n_shared, p->hidden_size, p->inter_size, p->group_size);
+  const bool decode = !general && decode_path_supported(T, k, Ep, p->n_shared, p->hidden_size,
+                                                       p->inter_size, p->group_size);
   int st = EXQ_SUCCESS;
   if (!decode) {
     st = record_stage(0, s);
@@ -615,6 +625,38 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     d.sync = reinterpret_cast<int*>(ws + L.sync);
     d.bf = bf;
     return launch_decode_layer(d, s);  // times its two kernels with the stage events
+  } else if (general) {
+    GemmArgs g{};
+    g.hdr = rp.hdr;
+    g.tg = rp.tg;
+    g.row_slot = rp.sorted;
+    g.slot_div = kp;
+    g.group_size = gs;
+    g.inter = I;
+    // gate/up + SiLU -> mid [n, I]; down -> partial [slot, H]
+    g.n_blocks = (int)cdiv(I, 16);
+    g.x = reinterpret_cast<const uint16_t*>(hidden);
+    g.x_stride = H;
+    g.K = H;
+    g.w = b13;
+    g.n_rows = 2 * I;
+    g.out = ws + L.mid;
+    g.out_stride = I;
+    st = launch_general_gemm(MODE_GATEUP, bf, g, L.tg_cap, s);
+    if (st) return st;
+    st = record_stage(2, s);
+    if (st) return st;
+    g.n_blocks = (int)cdiv(H, 16);
+    g.x = reinterpret_cast<const uint16_t*>(ws + L.mid);
+    g.x_stride = I;
+    g.K = I;
+    g.w = b2;
+    g.n_rows = H;
+    g.out = ws + L.partial;
+    g.out_stride = H;
+    g.H = H;
+    st = launch_general_gemm(MODE_DOWN, bf, g, L.tg_cap, s);
+    if (st) return st;
   } else {
     GemmArgs g{};
     g.hdr = rp.hdr;
@@ -709,14 +751,21 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
   EXQ_REQUIRE(is_act_dtype(act_dtype), "%s: act dtype must be f16 or bf16", fn);
   EXQ_REQUIRE(n_rows >= 0 && n_rows <= INT32_MAX && n_experts >= 1 && n_experts <= 1024,
               "%s: bad sizes", fn);
-  EXQ_REQUIRE_SUPPORTED(K >= 128 && K % 128 == 0, "%s: K=%lld must be a multiple of 128", fn,
-                        (long long)K);
-  EXQ_REQUIRE_SUPPORTED(N >= 32 && N % 32 == 0, "%s: N=%lld must be a multiple of 32", fn,
-                        (long long)N);
-  if (tier == 2)
-    EXQ_REQUIRE_SUPPORTED(gs >= 128 && gs % 128 == 0 && K % gs == 0,
-                          "%s: group_size=%lld must be a multiple of 128 dividing K", fn,
-                          (long long)gs);
+  // INT4 weights of other shapes (K % 32, a group size that is a multiple of
+  // 32 dividing K, any N) run on the general kernel; BF16 weights need the
+  // tiled / grouped kernels' shapes.
+  const bool general = tier == 2 && !(K % 128 == 0 && N % 32 == 0 && gs % 128 == 0);
+  if (tier == 2) {
+    EXQ_REQUIRE_SUPPORTED(general_shape(K, gs),
+                          "%s: K=%lld and group_size=%lld: the group size must be a multiple "
+                          "of 32 dividing K", fn, (long long)K, (long long)gs);
+    EXQ_REQUIRE_SUPPORTED(N >= 1 && N <= INT32_MAX, "%s: bad N=%lld", fn, (long long)N);
+  } else {
+    EXQ_REQUIRE_SUPPORTED(K >= 128 && K % 128 == 0, "%s: K=%lld must be a multiple of 128",
+                          fn, (long long)K);
+    EXQ_REQUIRE_SUPPORTED(N >= 32 && N % 32 == 0, "%s: N=%lld must be a multiple of 32", fn,
+                          (long long)N);
+  }
   const int64_t tg_cap = tg_capacity(n_rows, n_experts);
   const size_t tg_off = align_up(64, 256);
   const size_t rs_off = tg_off + align_up((size_t)tg_cap * sizeof(TgEntry), 256);
@@ -732,7 +781,7 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
   int* hdr = reinterpret_cast<int*>(ws);
   TgEntry* tg = reinterpret_cast<TgEntry*>(ws + tg_off);
   const bool bf = act_dtype == EXQ_DTYPE_BF16;
-  const bool tile = (tier == 2 || tier == 0) &&
+  const bool tile = !general && (tier == 2 || tier == 0) &&
                     tile_gemm_applies(tier, MODE_PLAIN, (int)N, 0, (int)K, (int)gs) &&
                     tile_rowsum_floats(n_rows, K) * 4 <= 0x7fffffffLL;
   int st = launch_tg_from_ends(ends, (int)n_experts, mask, tier,
@@ -750,6 +799,10 @@ int sorted_gemm_impl(const void* a_sorted, int act_dtype, int64_t n_rows, int64_
   g.group_size = (int)gs;
   g.out = c;
   g.out_stride = N;
+  if (general) {
+    g.n_blocks = (int)cdiv(N, 16);
+    return launch_general_gemm(MODE_PLAIN, bf, g, tg_cap, s);
+  }
   if (tile && tier == 0) return launch_tile_gemm(0, MODE_PLAIN, bf, g, nullptr, 0, 0, tg_cap, s);
   if (tile) {
     float* rs = reinterpret_cast<float*>(ws + rs_off);

@@ -99,10 +99,16 @@ def pack_experts_int4(expert_weights: torch.Tensor, group_size: int = 128,
 
 
 def _effective_group(K: int, scales: torch.Tensor) -> int:
+    """Group size implied by the scales' shape (moe_int4_kernel.py:274-277);
+    below 32 is rejected as the reference does (:286-290)."""
     n_groups = scales.shape[-1]
     if n_groups <= 0 or K % n_groups:
         raise ValueError(f"scales last dim {n_groups} does not divide K={K}")
-    return K // n_groups
+    g = K // n_groups
+    if g < 32:
+        raise ValueError(f"group_size={g} is too small (minimum 32): K={K} has {n_groups} "
+                         "scale groups")
+    return g
 
 
 def moe_int4_forward(hidden_states: torch.Tensor, expert_packed: torch.Tensor,

@@ -160,10 +160,13 @@ int exq_silu_and_mul(const void* input, int dtype, int64_t rows, int64_t inter,
  * registers (exact (q-8) values, fp32 group accumulation, fp16 group scale
  * applied in fp32).  Replaces the _moe_gemm_int4_kernel launch of
  * moe_int4_forward (exq/kernels/moe_int4_kernel.py:124-240, 303-326).
- * A and C: f16 | bf16 (same dtype).  Requires K % 128 == 0 and
- * group_size % 128 == 0, N % 32 == 0.  exq_moe_gemm_workspace_size covers
- * the token-group list and, for INT4 weights with N % 128 == 0 (the tiled
- * kernel), the per-row group sums of A (n_rows * K / 128 floats).
+ * A and C: f16 | bf16 (same dtype).  K % 32 == 0 and a group size that is a
+ * multiple of 32 dividing K (the reference's minimum group is 32,
+ * moe_int4_kernel.py:286-290); any N >= 1 (the reference masks the N tail).
+ * K, group_size multiples of 128 with N % 32 == 0 take the tiled / grouped
+ * kernels, other shapes the general kernel.  exq_moe_gemm_workspace_size
+ * covers the token-group list and, for INT4 weights with N % 128 == 0 (the
+ * tiled kernel), the per-row group sums of A (n_rows * K / 128 floats).
  */
 size_t exq_moe_gemm_workspace_size(int64_t n_rows, int64_t n_experts, int64_t K);
 int exq_moe_int4_gemm(const void* a_sorted, int act_dtype, int64_t n_rows, int64_t K,
@@ -212,7 +215,7 @@ typedef struct exq_moe_problem {
   int64_t n_experts;     /* E routed experts */
   int64_t top_k;         /* k */
   int64_t n_shared;      /* always-on experts, ids E..E+n_shared-1, weight 1 */
-  int64_t group_size;    /* INT4 group size (128) */
+  int64_t group_size;    /* INT4 group size: a multiple of 32 dividing H and I */
   int act_dtype;         /* hidden / out: f16 | bf16 */
   int ids_dtype;         /* i32 | i64 */
   int weights_dtype;     /* f32 | f16 | bf16 */
@@ -254,7 +257,10 @@ size_t exq_moe_workspace_size(const exq_moe_problem* problem);
  * SiLU-and-mul, down INT4 GEMM, top-k weighted combine.  Decode batches
  * (T <= 64) run as two kernels (gate/up + SiLU, down + combine) that route
  * for themselves; larger batches as routing plan + two grouped MFMA GEMMs +
- * combine.  Replaces the
+ * combine.  H, I multiples of 32 and a group size that is a multiple of 32
+ * dividing both; shapes whose H, I or group size is not a multiple of 128
+ * run as routing plan + the general kernels + combine at every batch size
+ * (the mixed-precision layer keeps the 128-multiples).  Replaces the
  * pipeline of _exq_forward_cuda (exq/runtime/sglang_backend.py:65-158:
  * moe_align_block_size -> build_ends_from_slots -> gather_hidden -> GEMM1 ->
  * silu_and_mul -> GEMM2 -> combine) and moe_int4_full_forward
