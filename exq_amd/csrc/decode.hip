@@ -5,7 +5,10 @@
 //   down kernel:    unit = (active expert, ROWS_B output rows); fp32 partial
 //                   rows per routed slot; the last unit to finish a column
 //                   block of H combines it over each token's slots in fixed
-//                   order (deterministic) and writes `out`.
+//                   order (deterministic) and writes `out`.  From T = 32 or
+//                   four k-splits on, that tail (one work-group per block)
+//                   outlasts a separate launch, so decode_combine_kernel does
+//                   the same combine as a third launch instead.
 //
 // Both kernels route for themselves: every work-group reads the (<= 1024)
 // routed ids into LDS once, marks the active experts in a bitmap and counts
@@ -63,6 +66,8 @@ constexpr int DW = 4;              // waves per work-group
 constexpr int DNT = DW * 64;
 constexpr int MAX_SLOTS = 1024;    // T * (k + n_shared)
 constexpr int MAX_BM_WORDS = 32;   // active-expert bitmap: E + shared <= 1024
+constexpr int kCombineLaunchMinT = 32;     // down combine: own launch from this batch on,
+constexpr int kCombineLaunchMinSplit = 4;  // or from this many k-splits on; else in-kernel
 
 // Output rows of a down unit: 64 (four row sets), 32 when a pass holds two
 // or four 16-row tiles (register budget of the accumulators).
@@ -107,6 +112,8 @@ struct LayerArgs {
   int* sync;                    // combine counters, see sync_* below
   int nbA, nbB;                 // units per expert: I / 16, H / rows_b(NT)
   int nsplit;                   // down: k-splits per (expert, row block), partial sets
+  int combine;                  // down: 1 = the last unit of a column block combines it,
+                                // 0 = decode_combine_kernel runs after the down kernel
 };
 
 // Counter layout of the sync region (fixed, independent of the problem size):
@@ -429,22 +436,14 @@ __device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TI
       }
       stored = true;
     }
-    if (stored) wait_vm_all();  // this wave's partial rows have completed
+    if (stored && a.combine) wait_vm_all();  // this wave's partial rows have completed
   }
 }
 
-// Down phase, after the unit's last pass: count the unit in for its column
-// block; the last of the block's units combines the block.
+// Down phase: the last of a column block's units (by its counter) combines
+// the block.
 template <bool BF, int ROWS_B>
-__device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Route& rt, int blk,
-                                                    int n_tiles, int* s_flag) {
-  if (threadIdx.x == 0) {  // n_tiles units (times the k-splits) write each column block
-    const int old =
-        __hip_atomic_fetch_add(sync_c(a, blk), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = old == n_tiles * a.nsplit - 1;
-  }
-  __syncthreads();
-  if (!*s_flag) return;
+__device__ __forceinline__ void combine_block(const LayerArgs& a, const Route& rt, int blk) {
   // out[t, h..h+3] = sum over the token's slots j (ascending) of weight *
   // partial; a chunk of eight slots' loads is issued at once
   const int64_t set = (int64_t)a.T * a.kp * a.H;  // floats per partial set
@@ -503,6 +502,21 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
     if (d == a.nbB - 1)  // every block is combined
       __hip_atomic_store(sync_done(a), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// Down phase, after the unit's last pass: count the unit in for its column
+// block (n_tiles units times the k-splits write each block); the last of the
+// block's units combines the block.
+template <bool BF, int ROWS_B>
+__device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Route& rt, int blk,
+                                                    int n_tiles, int* s_flag) {
+  if (threadIdx.x == 0) {
+    const int old =
+        __hip_atomic_fetch_add(sync_c(a, blk), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = old == n_tiles * a.nsplit - 1;
+  }
+  __syncthreads();
+  if (*s_flag) combine_block<BF, ROWS_B>(a, rt, blk);
 }
 
 // INT4 unit whose k-blocks fit the wave's LDS region (nmy <= CK): every
@@ -1157,8 +1171,71 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
       else
         run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
     }
-    if constexpr (PH == 1) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_tiles, &s_flag);
+    if constexpr (PH == 1)
+      if (a.combine) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_tiles, &s_flag);
   }
+}
+
+// The down phase's combine as a launch of its own (LayerArgs::combine == 0):
+// out[t, h..h+3] = sum over the token's slots j (ascending) of weight * the
+// slot's partial row (its k-splits summed in split order first), fp32,
+// rounded once -- the same order and arithmetic as combine_block.  One thread
+// per four consecutive h; the kernel boundary makes every partial row visible.
+template <bool BF>
+__global__ void __launch_bounds__(256) decode_combine_kernel(LayerArgs a) {
+  const int hq = a.H >> 2;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.T * hq) return;
+  const int t = idx / hq;
+  const int h = (idx - t * hq) * 4;
+  const int64_t set = (int64_t)a.T * a.kp * a.H;  // floats per partial set
+  const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, a.nsplit * set * 4);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  // eight slots at a time: their ids and weights, then every partial load of
+  // the chunk in flight at once (dropped slots load zeros: out-of-range offset)
+  for (int j0 = 0; j0 < a.kp; j0 += 8) {
+    float wg[8];
+    int off[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const int j = j0 + jj;
+      bool ok = j < a.kp;
+      float wgt = 1.f;
+      if (ok && j < a.k) {
+        const int64_t id = load_index(a.ids, a.ids_dtype, (int64_t)t * a.k + j);
+        wgt = load_as_f32(a.topk_w, a.w_dtype, (int64_t)t * a.k + j);
+        ok = id >= 0 && id < a.E;
+      }
+      wg[jj] = ok ? wgt : 0.f;
+      off[jj] = ok ? ((t * a.kp + j) * a.H + h) * 4 : OOB_OFF;
+    }
+    float4 pv[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      pv[jj] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(part_r, off[jj], 0, 0));
+    for (int sp = 1; sp < a.nsplit; ++sp) {  // further k-splits, in split order
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const float4 q = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(
+                        part_r, off[jj] == OOB_OFF ? OOB_OFF : (int)(off[jj] + sp * set * 4), 0, 0));
+        pv[jj].x += q.x; pv[jj].y += q.y; pv[jj].z += q.z; pv[jj].w += q.w;
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      if (j0 + jj < a.kp) {
+        acc[0] += wg[jj] * pv[jj].x;
+        acc[1] += wg[jj] * pv[jj].y;
+        acc[2] += wg[jj] * pv[jj].z;
+        acc[3] += wg[jj] * pv[jj].w;
+      }
+    }
+  }
+  uint2 o;
+  o.x = to_act_bits<BF>(acc[0]) | (to_act_bits<BF>(acc[1]) << 16);
+  o.y = to_act_bits<BF>(acc[2]) | (to_act_bits<BF>(acc[3]) << 16);
+  *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.H + h) = o;
 }
 
 typedef void (*decode_kernel_t)(LayerArgs);
@@ -1251,6 +1328,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   a.nbA = d.I / 16;
   a.nbB = d.H / rows_b(nt);
   a.nsplit = 1;
+
   const int64_t max_active = (int64_t)(d.T * d.k < d.E ? d.T * d.k : d.E) + (d.Ep - d.E);
   // Tiles: at most one per active expert plus one per further 16 rows.  The
   // grid is sized for one tile per expert up to T = 16 (more tiles there
@@ -1273,6 +1351,14 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
       if (sp > cap) sp = cap;
       if (sp > kDecodeMaxSplit) sp = kDecodeMaxSplit;
       a.nsplit = sp < 1 ? 1 : (int)sp;
+      // The last unit of each column block combines it inside the down
+      // kernel for small batches; from kCombineLaunchMinT tokens or
+      // kCombineLaunchMinSplit k-splits on, that tail (one work-group per
+      // block reading T x kp x nsplit partial rows) outlasts a separate, fully
+      // parallel combine launch (measured: Qwen3 T=64 81.2 -> 73.5 µs/layer,
+      // Mixtral T=1 66.7 -> 63.2; T <= 16 with few splits 0.5-1 µs better
+      // in-kernel).
+      a.combine = d.T < kCombineLaunchMinT && a.nsplit < kCombineLaunchMinSplit ? 1 : 0;
     }
     // INT4 slices go through LDS when every wave's k-range fits its region
     const int rs = ph == 0 ? 2 : rows_b(nt) / 16;
@@ -1300,12 +1386,27 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     if (st0) return st0;
     const int64_t grid = units < resident ? units : resident;
     const dim3 g((unsigned)(grid > 0 ? grid : 1));
-    if (const hipEvent_t* ev = stage_events())  // start / stop of exactly this kernel
-      hipExtLaunchKernelGGL(kern, g, dim3(DNT), klds, s, ev[2 * ph], ev[2 * ph + 1], 0, a);
+    // stage events: start / stop of exactly this kernel (the down stage ends
+    // after the combine launch when there is one)
+    const hipEvent_t* ev = stage_events();
+    const bool tail = ph == 1 && !a.combine;
+    if (ev)
+      hipExtLaunchKernelGGL(kern, g, dim3(DNT), klds, s, ev[2 * ph],
+                            tail ? nullptr : ev[2 * ph + 1], 0, a);
     else
       hipLaunchKernelGGL(kern, g, dim3(DNT), klds, s, a);
-    const int st = check_launch(ph == 0 ? "moe_decode_kernel<gate/up>" : "moe_decode_kernel<down>");
+    int st = check_launch(ph == 0 ? "moe_decode_kernel<gate/up>" : "moe_decode_kernel<down>");
     if (st) return st;
+    if (tail) {
+      const dim3 cg((unsigned)cdiv((int64_t)d.T * (d.H / 4), 256));
+      const auto ck = d.bf ? decode_combine_kernel<true> : decode_combine_kernel<false>;
+      if (ev)
+        hipExtLaunchKernelGGL(ck, cg, dim3(256), 0, s, nullptr, ev[3], 0, a);
+      else
+        hipLaunchKernelGGL(ck, cg, dim3(256), 0, s, a);
+      st = check_launch("decode_combine_kernel");
+      if (st) return st;
+    }
   }
   return EXQ_SUCCESS;
 }

@@ -25,7 +25,7 @@ def _capture(fn):
     return g, out
 
 
-@pytest.mark.parametrize("T", [16, 300])
+@pytest.mark.parametrize("T", [16, 64, 300])
 def test_graph_replays_int4_layer(T, device):
     from exq_amd.kernels import fused_experts, fused_topk, pack_experts_int4
     from exq_amd.kernels.fused_moe import moe_workspace_bytes
