@@ -69,6 +69,7 @@ _SIGNATURES = {
     "exq_set_stage_events": ([C.POINTER(C.c_void_p), _INT], _INT),
     "exq_pack_int4": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P], _INT),
     "exq_quantize_int8": ([_P, _INT, _I64, _I64, _P, _P, _P], _INT),
+    "exq_fake_quant": ([_P, _INT, _I64, _I64, _INT, _I64, _P, _P], _INT),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
@@ -141,8 +142,8 @@ def require_gpu(*tensors: torch.Tensor) -> torch.device:
 # Per-(device, stream, kind) workspace cache: reused across calls on one
 # stream, which is safe because launches on one stream are ordered.  The
 # fused-layer workspace ("fused") is kept apart from the scratch of the other
-# entry points: its first bytes hold counters that must stay zero between
-# calls, and the fused kernels leave them zero.
+# entry points (its first bytes hold the decode kernels' combine counters,
+# which each fused call clears itself).
 _ws_cache: dict[tuple[int, int, str], torch.Tensor] = {}
 
 

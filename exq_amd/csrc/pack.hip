@@ -112,10 +112,86 @@ __global__ void __launch_bounds__(256) quant_int8_kernel(const void* __restrict_
   if (threadIdx.x == 0) scales[row] = (uint16_t)f32_to_f16_bits(scale);
 }
 
+// Store v (fp32) in the weights' dtype, rounded to nearest even.
+__device__ __forceinline__ void store1(void* out, int dtype, int64_t i, float v) {
+  if (dtype == EXQ_DTYPE_F32)
+    reinterpret_cast<float*>(out)[i] = v;
+  else if (dtype == EXQ_DTYPE_BF16)
+    reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_bf16_bits(v);
+  else
+    reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_f16_bits(v);
+}
+
+// Fake quantisation (quantise then dequantise in place of the weights):
+// INT4 per group of g along the row (a short last group counts as padded with
+// zeros), INT8 per row; out = q * scale with the fp32 scale, in the weights'
+// dtype.  One wave per (row, group) for INT4 (g <= 512, lanes stride the
+// group), one work-group per row for INT8.
+// (`out` may alias `w`: each element is read, then written, by one lane.)
+__global__ void __launch_bounds__(256) fake_int4_kernel(const void* w, int dtype, int64_t rows,
+                                                        int K, int g, void* out) {
+  const int ng = (K + g - 1) / g;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= rows * ng) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int64_t row = unit / ng;
+  const int k0 = (int)(unit - row * ng) * g;
+  const int k1 = k0 + g < K ? k0 + g : K;
+  const int64_t base = row * K;
+  float m = 0.f;
+  for (int k = k0 + lane; k < k1; k += 64) m = fmaxf(m, fabsf(load1(w, dtype, base + k)));
+  for (int d = 1; d < 64; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  const float scale = fmaxf(m / 7.0f, kFp32Eps);
+  for (int k = k0 + lane; k < k1; k += 64) {
+    const float q = fminf(fmaxf(rintf(load1(w, dtype, base + k) / scale), -8.f), 7.f);
+    store1(out, dtype, base + k, q * scale);
+  }
+}
+
+__global__ void __launch_bounds__(256) fake_int8_kernel(const void* w, int dtype, int K,
+                                                        void* out) {
+  __shared__ float red[4];
+  const int64_t base = (int64_t)blockIdx.x * K;
+  float m = 0.f;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(load1(w, dtype, base + k)));
+  for (int d = 1; d < 64; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float scale = fmaxf(m / 127.0f, kFp32Eps);
+  for (int k = threadIdx.x; k < K; k += blockDim.x) {
+    const float q = fminf(fmaxf(rintf(load1(w, dtype, base + k) / scale), -128.f), 127.f);
+    store1(out, dtype, base + k, q * scale);
+  }
+}
+
 }  // namespace
 }  // namespace exq
 
 using namespace exq;
+
+extern "C" int exq_fake_quant(const void* weights, int dtype, int64_t rows, int64_t K, int bits,
+                              int64_t group_size, void* out, exq_stream stream) {
+  const char* fn = "exq_fake_quant";
+  EXQ_REQUIRE(is_float_dtype(dtype), "%s: dtype must be f32, f16 or bf16", fn);
+  EXQ_REQUIRE(bits == 4 || bits == 8, "%s: bits must be 4 or 8 (got %d)", fn, bits);
+  EXQ_REQUIRE(rows >= 0 && rows <= INT32_MAX && K >= 1 && K <= INT32_MAX, "%s: bad sizes", fn);
+  EXQ_REQUIRE(bits == 8 || (group_size >= 1 && group_size <= 512),
+              "%s: group_size=%lld must be in [1, 512]", fn, (long long)group_size);
+  if (rows == 0) return EXQ_SUCCESS;
+  EXQ_REQUIRE(weights && out, "%s: null pointer", fn);
+  hipStream_t s = as_stream(stream);
+  if (bits == 4) {
+    const int64_t units = rows * cdiv(K, group_size);
+    EXQ_REQUIRE(cdiv(units, 4) <= INT32_MAX, "%s: too many groups", fn);
+    hipLaunchKernelGGL(fake_int4_kernel, dim3((unsigned)cdiv(units, 4)), dim3(256), 0, s, weights,
+                       dtype, rows, (int)K, (int)group_size, out);
+  } else {
+    hipLaunchKernelGGL(fake_int8_kernel, dim3((unsigned)rows), dim3(256), 0, s, weights, dtype,
+                       (int)K, out);
+  }
+  return check_launch(fn);
+}
 
 extern "C" int exq_pack_int4(const void* weights, int dtype, int64_t rows, int64_t K,
                              int64_t group_size, uint8_t* packed, uint16_t* scales,

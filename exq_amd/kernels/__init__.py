@@ -11,6 +11,7 @@ from .moe_int4_kernel import (moe_int4_forward, moe_int4_full_forward, pack_expe
                               pack_int4_weights)
 from . import exq_dispatch
 from .exq_dispatch import fused_topk
+from .quant_shim import quantize_tensor_int4, quantize_tensor_int8
 
 __all__ = [
     "moe_grouped_gemm",
@@ -28,4 +29,6 @@ __all__ = [
     "quantize_int8_rows",
     "exq_dispatch",
     "fused_topk",
+    "quantize_tensor_int4",
+    "quantize_tensor_int8",
 ]

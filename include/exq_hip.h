@@ -206,6 +206,20 @@ int exq_pack_int4(const void* weights, int dtype, int64_t rows, int64_t K,
 int exq_quantize_int8(const void* weights, int dtype, int64_t rows, int64_t K, int8_t* q,
                       uint16_t* scales, exq_stream stream);
 
+/*
+ * Fake quantisation of [rows, K] weights (f32 | f16 | bf16) into `out` (same
+ * shape and dtype; may alias `weights`): quantise then dequantise, the
+ * accuracy-simulation path of quantize_tensor_int4 / quantize_tensor_int8
+ * (exq/eval/quant_shim.py:84-125).  bits = 4: per group of group_size along
+ * the row (the reference uses 128 and pads a short last group with zeros,
+ * which leaves its max|w| unchanged), scale = max|w| / 7; bits = 8: per row,
+ * scale = max|w| / 127.  Scales in fp32 (IEEE division) floored at fp32 eps,
+ * q = round-half-even(w / scale) clamped to [-8, 7] / [-128, 127], out =
+ * q * scale rounded once to the dtype.
+ */
+int exq_fake_quant(const void* weights, int dtype, int64_t rows, int64_t K, int bits,
+                   int64_t group_size, void* out, exq_stream stream);
+
 /* ---- fused MoE layer ----------------------------------------------------- */
 
 typedef struct exq_moe_problem {
