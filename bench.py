@@ -16,7 +16,8 @@ timed with HIP events recorded on its stream around it, over >= 300 layer
 calls), the OLMoE T=16 line (`north_star`: BASELINE.json configs[0], the
 target configuration, with its own kernel roofline), the decode-batch sweep
 (1, 4, 16, 64), the other configurations (P50 / P5 / P95 over >= 300 layer
-calls each) and the reference's CPU path timed on this host at every
+calls each), the streaming-read ceiling of this box (exq_stream_read over
+2 GiB) and the reference's CPU path timed on this host at every
 configuration, both variants (`cpu_baseline.configs`).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--batch 16]
@@ -559,6 +560,36 @@ def measure_configs(dev, reps, cpu=None):
     return rows, north_star, cpu_rows
 
 
+def stream_read_ceiling(dev, nbytes=2 << 30, reps=10):
+    """HBM streaming-read rate (GB/s) of exq_stream_read over a buffer far
+    larger than the 256 MB Infinity Cache: the read rate a kernel on this box
+    can reach, beside the 8 TB/s data-sheet peak."""
+    import torch
+    from exq_amd import _lib
+    L = _lib.lib()
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(8192, dtype=torch.int32, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def run():
+        _lib.check(L.exq_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), sink.numel(),
+                                     stream), "exq_stream_read")
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del buf, sink
+    return {"GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes, "reps": reps,
+            "kernel": "exq_stream_read (16-byte loads, 8 in flight per thread)"}
+
+
 def cpu_model():
     """lscpu-style model name of the host CPU."""
     try:
@@ -682,6 +713,8 @@ def main():
     kern_bytes = stack.w13_bytes * sum(b.active) / len(b.active)
     kern_gbps = kern_bytes / (kern_us * 1e-6) / 1e9
     traffic = traffic_from_profile("qwen3", args.batch)
+    ceiling = stream_read_ceiling(dev)
+    log(f"streaming-read ceiling: {ceiling['GBps']:.0f} GB/s")
 
     sweep = []
     for T in [int(v) for v in args.sweep.split(",") if v.strip()]:
@@ -755,7 +788,9 @@ def main():
                      "kernel": "moe_decode_kernel<bf16, gate/up, NT=1, INT4 LDS path>",
                      "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "bytes_per_launch": round(kern_bytes), "launch_us": round(kern_us, 3)},
+                     "bytes_per_launch": round(kern_bytes), "launch_us": round(kern_us, 3),
+                     "frac_of_stream_ceiling": round(kern_gbps / ceiling["GBps"], 4)},
+        "stream_read_ceiling": ceiling,
         "stages_us": {k: round(v, 3) for k, v in st.items()},
         "north_star": north_star,
         "sweep": sweep,

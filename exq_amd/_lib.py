@@ -70,6 +70,7 @@ _SIGNATURES = {
     "exq_pack_int4": ([_P, _INT, _I64, _I64, _I64, _P, _P, _P], _INT),
     "exq_quantize_int8": ([_P, _INT, _I64, _I64, _P, _P, _P], _INT),
     "exq_fake_quant": ([_P, _INT, _I64, _I64, _INT, _I64, _P, _P], _INT),
+    "exq_stream_read": ([_P, _I64, _P, _I64, _P], _INT),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -90,6 +90,51 @@ __global__ void __launch_bounds__(256) silu_mul_kernel(const void* __restrict__ 
 
 using namespace exq;
 
+namespace exq {
+namespace {
+
+// Streaming-read ceiling: every thread reads 16-byte pieces grid-strided, 8 in
+// flight per iteration, and folds them into one word per work-group (so no
+// load is dead).
+__global__ void __launch_bounds__(256) stream_read_kernel(const uint4* __restrict__ buf,
+                                                          int64_t n16,
+                                                          uint32_t* __restrict__ sink) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  uint32_t acc = 0;
+  for (; i + 7 * stride < n16; i += 8 * stride) {
+    uint4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = buf[i + j * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 v = buf[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  for (int d = 1; d < 64; d <<= 1) acc ^= __shfl_xor(acc, d, 64);
+  if ((threadIdx.x & 63) == 0) atomicXor(&sink[blockIdx.x], acc);
+}
+
+}  // namespace
+}  // namespace exq
+
+extern "C" int exq_stream_read(const void* buf, int64_t bytes, uint32_t* sink, int64_t sink_words,
+                               exq_stream stream) {
+  const char* fn = "exq_stream_read";
+  EXQ_REQUIRE(bytes >= 0 && bytes % 16 == 0, "%s: bytes=%lld must be a multiple of 16", fn,
+              (long long)bytes);
+  EXQ_REQUIRE(sink_words >= 1, "%s: need a sink word per work-group", fn);
+  if (bytes == 0) return EXQ_SUCCESS;
+  EXQ_REQUIRE(buf && sink && (uintptr_t)buf % 16 == 0, "%s: null or misaligned pointer", fn);
+  const int64_t grid = sink_words < 8192 ? sink_words : 8192;
+  hipLaunchKernelGGL(exq::stream_read_kernel, dim3((unsigned)grid), dim3(256), 0,
+                     exq::as_stream(stream), reinterpret_cast<const uint4*>(buf), bytes / 16,
+                     sink);
+  return exq::check_launch(fn);
+}
+
 extern "C" int exq_abi_version(void) { return EXQ_ABI_VERSION; }
 
 extern "C" const char* exq_last_error(void) { return g_last_error; }

@@ -340,6 +340,17 @@ int exq_moe_int4_fused_forward_noalloc(const exq_moe_problem* problem, const voi
  */
 int exq_set_stage_events(void* const* events, int n_events);
 
+/*
+ * Measurement hook (no counterpart in the reference): the streaming-read
+ * ceiling.  Reads `bytes` (a multiple of 16) from `buf` with 16-byte loads,
+ * grid-strided over min(sink_words, 8192) work-groups of 256 threads, and
+ * XORs each work-group's fold into sink[work-group] (so nothing is dead);
+ * bench.py times it on a buffer far larger than the Infinity Cache to report
+ * the HBM read rate the decode kernels are measured against.
+ */
+int exq_stream_read(const void* buf, int64_t bytes, uint32_t* sink, int64_t sink_words,
+                    exq_stream stream);
+
 #ifdef __cplusplus
 }
 #endif
