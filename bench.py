@@ -17,7 +17,9 @@ calls), the OLMoE T=16 line (`north_star`: BASELINE.json configs[0], the
 target configuration, with its own kernel roofline), the decode-batch sweep
 (1, 4, 16, 64), the other configurations (P50 / P5 / P95 over >= 300 layer
 calls each), the streaming-read ceiling of this box (exq_stream_read over
-2 GiB) and the reference's CPU path timed on this host at every
+2 GiB), a plain streaming read of exactly the dominant kernel's bytes per
+launch (48 distinct buffers replayed from a graph: the floor at that
+transfer size) and the reference's CPU path timed on this host at every
 configuration, both variants (`cpu_baseline.configs`).
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--batch 16]
@@ -590,6 +592,48 @@ def stream_read_ceiling(dev, nbytes=2 << 30, reps=10):
             "kernel": "exq_stream_read (16-byte loads, 8 in flight per thread)"}
 
 
+def stream_read_at_size(dev, nbytes, n_bufs=48, reps=5, grid=2048):
+    """Plain streaming read of `nbytes` (a kernel's bytes per launch) with
+    exq_stream_read: n_bufs distinct buffers (together beyond the 256 MB
+    Infinity Cache) read back to back in one HIP graph, as the decode layers
+    are.  The time per read is the floor a kernel moving those bytes meets at
+    this transfer size (launch and ramp included)."""
+    import torch
+    from exq_amd import _lib
+    L = _lib.lib()
+    nbytes = nbytes // 16 * 16
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n_bufs)]
+    sink = torch.zeros(grid, dtype=torch.int32, device=dev)
+    s = torch.cuda.Stream()
+
+    def run():
+        h = s.cuda_stream
+        for bb in bufs:
+            _lib.check(L.exq_stream_read(bb.data_ptr(), nbytes, sink.data_ptr(), grid, h),
+                       "exq_stream_read")
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * n_bufs)
+    del g, bufs, sink
+    torch.cuda.empty_cache()
+    return {"bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "reads_timed": reps * n_bufs, "grid": grid}
+
+
 def cpu_model():
     """lscpu-style model name of the host CPU."""
     try:
@@ -715,6 +759,9 @@ def main():
     traffic = traffic_from_profile("qwen3", args.batch)
     ceiling = stream_read_ceiling(dev)
     log(f"streaming-read ceiling: {ceiling['GBps']:.0f} GB/s")
+    floor = stream_read_at_size(dev, int(kern_bytes))
+    log(f"streaming read of the kernel's {floor['bytes']} bytes: {floor['us']:.2f} us "
+        f"({floor['GBps']:.0f} GB/s)")
 
     sweep = []
     for T in [int(v) for v in args.sweep.split(",") if v.strip()]:
@@ -789,8 +836,11 @@ def main():
                      "achieved": round(kern_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(kern_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": round(kern_bytes), "launch_us": round(kern_us, 3),
-                     "frac_of_stream_ceiling": round(kern_gbps / ceiling["GBps"], 4)},
+                     "frac_of_stream_ceiling": round(kern_gbps / ceiling["GBps"], 4),
+                     "stream_read_same_bytes_us": floor["us"],
+                     "frac_of_stream_same_bytes": round(floor["us"] / kern_us, 4)},
         "stream_read_ceiling": ceiling,
+        "stream_read_same_bytes": floor,
         "stages_us": {k: round(v, 3) for k, v in st.items()},
         "north_star": north_star,
         "sweep": sweep,
