@@ -414,67 +414,110 @@ int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, 
 // taken on the logits themselves (largest first, equal logits to the lower
 // expert id): the ids never depend on how exp() rounds.  The denominator is
 // a fixed-order wave reduction (deterministic).
-template <int MAXC>  // logits per lane: E <= 64 * MAXC
+// Wave-wide reductions with DPP (gfx9 row forms): quad swaps, rotations by 4
+// and 8 inside each 16-lane row, then rows folded into row 3 by the row-15 and
+// row-31 broadcasts; lane 63 ends with the result, read back as a scalar.
+// `ID` is the operation's identity, returned by lanes a step does not write.
+template <int CTRL, int ROWS, uint32_t ID>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)ID, (int)v, CTRL, ROWS, 0xf, false);
+}
+template <uint32_t ID, typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, Op op) {
+  v = op(v, dpp_u32<0xB1, 0xf, ID>(v));   // quad_perm [1, 0, 3, 2]
+  v = op(v, dpp_u32<0x4E, 0xf, ID>(v));   // quad_perm [2, 3, 0, 1]
+  v = op(v, dpp_u32<0x124, 0xf, ID>(v));  // row_ror 4
+  v = op(v, dpp_u32<0x128, 0xf, ID>(v));  // row_ror 8
+  v = op(v, dpp_u32<0x142, 0xa, ID>(v));  // row_bcast 15 -> rows 1, 3
+  v = op(v, dpp_u32<0x143, 0xc, ID>(v));  // row_bcast 31 -> rows 2, 3
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  return __uint_as_float(wave_reduce_u32<0u>(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
+  }));
+}
+
+// Order-preserving key of a logit (larger logit, larger key; -0 and +0 share
+// one, as they compare equal); key 0 lies below every logit and marks an
+// expert that is taken or absent.
+__device__ __forceinline__ uint32_t logit_key(float x) {
+  uint32_t b = __float_as_uint(x);
+  if ((b << 1) == 0u) b = 0u;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float key_logit(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// One wave per token: lane l holds logits l, l + 64, ...  Each of the k rounds
+// takes the largest remaining logit (equal logits: the lower id) with one DPP
+// maximum over the lanes' best keys, and a DPP minimum over the ids only when
+// several lanes hold that key.
+template <int MAXC>
 __global__ void __launch_bounds__(256) topk_softmax_kernel(const void* logits, int ldt, int T,
                                                           int E, int k, int renorm, void* ids,
                                                           int idt, void* wts, int wdt) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= T) return;  // (wave-uniform)
-  float v[MAXC];
-  float m = -INFINITY;
+  const auto umax = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  const auto umin = [](uint32_t x, uint32_t y) { return x < y ? x : y; };
+  uint32_t key[MAXC];
+  uint32_t kmax = 0u;
 #pragma unroll
   for (int c = 0; c < MAXC; ++c) {
     const int e = lane + 64 * c;
-    v[c] = e < E ? load_as_f32(logits, ldt, (int64_t)row * E + e) : -INFINITY;
-    m = fmaxf(m, v[c]);
+    key[c] = e < E ? logit_key(load_as_f32(logits, ldt, (int64_t)row * E + e)) : 0u;
+    kmax = umax(kmax, key[c]);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  const float m = key_logit(wave_reduce_u32<0u>(kmax, umax));
   float sum = 0.f;
 #pragma unroll
   for (int c = 0; c < MAXC; ++c)
-    if (lane + 64 * c < E) sum += expf(v[c] - m);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
-  const float inv = 1.0f / sum;
-  uint32_t taken = 0u;  // bit c: logit c of this lane already chosen
-  float mine = 0.f;     // lane j < k: weight of the j-th choice
+    if (lane + 64 * c < E) sum += expf(key_logit(key[c]) - m);
+  const float inv = 1.0f / wave_sum_f32(sum);
+  float mine = 0.f;  // lane j < k: weight of the j-th choice
+  int my_id = 0;     // lane j < k: id of the j-th choice
+  float ws = 0.f;    // sum of the chosen weights, in choice order
   for (int j = 0; j < k; ++j) {
-    float bv = -INFINITY;
-    int be = INT32_MAX;
+    uint32_t bk = 0u;
+    int bc = 0;
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      const int e = lane + 64 * c;
-      if (e < E && !((taken >> c) & 1u) && (v[c] > bv || be == INT32_MAX)) {
-        bv = v[c];
-        be = e;
+    for (int c = 0; c < MAXC; ++c)
+      if (key[c] > bk) {  // strict: the lower c (lower id) keeps a tie
+        bk = key[c];
+        bc = c;
       }
+    const uint32_t K = wave_reduce_u32<0u>(bk, umax);
+    const uint64_t at = __ballot(bk == K);
+    int be;
+    if (__popcll(at) == 1) {
+      const int l = __builtin_amdgcn_readfirstlane(__ffsll((unsigned long long)at) - 1);
+      be = __builtin_amdgcn_readlane(lane + 64 * bc, l);
+    } else {
+      be = (int)wave_reduce_u32<0xffffffffu>(bk == K ? (uint32_t)(lane + 64 * bc) : 0xffffffffu, umin);
     }
+    if ((be & 63) == lane) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {  // larger logit, then lower id
-      const float ov = __shfl_xor(bv, o, 64);
-      const int oe = __shfl_xor(be, o, 64);
-      if (ov > bv || (ov == bv && oe < be)) {
-        bv = ov;
-        be = oe;
-      }
+      for (int c = 0; c < MAXC; ++c)
+        if (c == (be >> 6)) key[c] = 0u;
     }
-    if ((be & 63) == lane) taken |= 1u << (be >> 6);
-    if (lane == j) mine = expf(bv - m) * inv;
-    if (lane == 0) {
-      if (idt == EXQ_DTYPE_I64)
-        reinterpret_cast<int64_t*>(ids)[(int64_t)row * k + j] = be;
-      else
-        reinterpret_cast<int32_t*>(ids)[(int64_t)row * k + j] = be;
+    const float w = expf(key_logit(K) - m) * inv;
+    ws += w;
+    if (lane == j) {
+      mine = w;
+      my_id = be;
     }
   }
-  if (renorm) {  // sum of the k weights in choice order
-    float ws = 0.f;
-    for (int j = 0; j < k; ++j) ws += __shfl(mine, j, 64);
-    mine = mine / ws;
+  if (renorm) mine = mine / ws;
+  if (lane < k) {
+    if (idt == EXQ_DTYPE_I64)
+      reinterpret_cast<int64_t*>(ids)[(int64_t)row * k + lane] = my_id;
+    else
+      reinterpret_cast<int32_t*>(ids)[(int64_t)row * k + lane] = my_id;
+    store_from_f32(wts, wdt, (int64_t)row * k + lane, mine);
   }
-  if (lane < k) store_from_f32(wts, wdt, (int64_t)row * k + lane, mine);
 }
 
 }  // namespace exq
