@@ -206,6 +206,8 @@ extern "C" int exq_pack_int4(const void* weights, int dtype, int64_t rows, int64
               (long long)K, (long long)g);
   if (rows == 0) return EXQ_SUCCESS;
   EXQ_REQUIRE(weights && packed && scales, "%s: null pointer", fn);
+  EXQ_REQUIRE(cdiv(rows * (K / 2), 256) <= INT32_MAX, "%s: %lld x %lld weights is too large", fn,
+              (long long)rows, (long long)K);
   const int tpg = (int)(g / 8);
   const bool fast = g % 8 == 0 && tpg <= 64 && (tpg & (tpg - 1)) == 0 &&
                     ((uintptr_t)weights % 16 == 0) && ((uintptr_t)packed % 4 == 0);

@@ -308,19 +308,34 @@ __global__ void __launch_bounds__(RT) route_scan_kernel(RoutePlanParams p, int n
   __shared__ RouteLds s;
   const int nb = p.Ep;
   const int b = threadIdx.x;
+  // the bucket's per-block counts, 16 loads in flight at a time (a loop of
+  // single loads would wait out one memory latency per block)
+  constexpr int CB = 16;
   int tot_b = 0;
-  if (b < nb)
-    for (int k = 0; k < nblk; ++k) tot_b += p.blk_cnt[(int64_t)k * nb + b];
-  if (b < nb) s.cnt[b] = tot_b;
+  if (b < nb) {
+    for (int k0 = 0; k0 < nblk; k0 += CB) {
+      int cv[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j) cv[j] = k0 + j < nblk ? p.blk_cnt[(int64_t)(k0 + j) * nb + b] : 0;
+#pragma unroll
+      for (int j = 0; j < CB; ++j) tot_b += cv[j];
+    }
+    s.cnt[b] = tot_b;
+  }
   int t;
   const int ex = block_excl_scan(b < nb ? tot_b : 0, s.wsum, &t);
   if (b < nb) {
     s.start[b] = ex;
     int run = ex;
-    for (int k = 0; k < nblk; ++k) {  // counts -> offsets, in place
-      const int c = p.blk_cnt[(int64_t)k * nb + b];
-      p.blk_cnt[(int64_t)k * nb + b] = run;
-      run += c;
+    for (int k0 = 0; k0 < nblk; k0 += CB) {  // counts -> offsets, in place
+      int cv[CB];
+#pragma unroll
+      for (int j = 0; j < CB; ++j) cv[j] = k0 + j < nblk ? p.blk_cnt[(int64_t)(k0 + j) * nb + b] : 0;
+#pragma unroll
+      for (int j = 0; j < CB; ++j) {
+        if (k0 + j < nblk) p.blk_cnt[(int64_t)(k0 + j) * nb + b] = run;
+        run += cv[j];
+      }
     }
   }
   if (threadIdx.x == 0) s.start[nb] = t;
