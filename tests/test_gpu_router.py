@@ -61,6 +61,9 @@ def test_router_dtypes_and_ties(ldt, wdt, device):
     logits = torch.from_numpy(rng.standard_normal((50, 64)).astype(np.float32)).to(ldt)
     logits[3] = 0.0                       # every expert tied: ids 0..k-1
     logits[4, 10:20] = 5.0                # a tied block at the top
+    logits[5] = -1.0                      # +0 and -0 compare equal: a tie, lower ids first
+    logits[5, 20:30:2] = 0.0
+    logits[5, 21:31:2] = -0.0
     rtol = 2e-6 if wdt == torch.float32 else 1e-2
     _check(logits, 8, True, w_dtype=wdt, rtol=rtol)
     _check(logits, 8, False, w_dtype=wdt, rtol=rtol)
@@ -68,6 +71,7 @@ def test_router_dtypes_and_ties(ldt, wdt, device):
     _, ids = fused_topk(logits.cuda(), 8, False)
     assert ids[3].tolist() == list(range(8))
     assert ids[4].tolist() == list(range(10, 18))
+    assert ids[5].tolist() == list(range(20, 28))
 
 
 def test_router_masked_experts_and_edges(device):
