@@ -689,6 +689,7 @@ def cpu_baseline(deq, b, cpu):
 
 
 def main():
+    from exq_amd.eval import latency_stats
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -827,6 +828,9 @@ def main():
                      f"({args.steps * args.layers} layer calls)",
         "p5_us": round(pct(per_layer, 5), 3),
         "p95_us": round(pct(per_layer, 95), 3),
+        # the reference harness's statistics (exq/eval/bench.py) of the same series
+        "latency_stats_us": {k: (round(v, 3) if isinstance(v, float) else v)
+                             for k, v in latency_stats(per_layer).items()},
         "mean_us": round(ms * 1e3 / args.layers, 3),
         "tokens_per_s": round(args.batch / (us_layer * 1e-6)),
         "achieved_GBps": round(gbps, 1),
