@@ -116,9 +116,11 @@ int launch_route_plan(const RoutePlanParams& p, hipStream_t stream);
 int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, int tier,
                         int group, int* hdr, TgEntry* tg, int tg_cap, hipStream_t stream);
 
-// One-launch decode layer (decode.hip): routing, gate/up + SiLU, down and the
-// combine in a single persistent kernel.  `sync` points at the zero-filled
-// counter region (kDecodeSyncBytes at the start of the fused workspace).
+// Decode layer (decode.hip, T <= 64): a gate/up + SiLU kernel and a down
+// kernel that route for themselves, the down kernel combining in-kernel or
+// through a third, combine launch.  `sync` points at the combine counters
+// (kDecodeSyncBytes at the start of the fused workspace); the gate/up kernel
+// clears them, so the region needs no zero fill.
 constexpr int kDecodeMaxBuckets = 1024;   // routed + shared experts
 constexpr int kDecodeMaxHBlocks = 512;    // H / 64
 constexpr size_t kDecodeSyncBytes = (size_t)(kDecodeMaxBuckets + kDecodeMaxHBlocks + 2) * 128;
