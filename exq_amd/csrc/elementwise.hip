@@ -53,13 +53,14 @@ __global__ void inverse_perm_kernel(const int64_t* __restrict__ order, int n,
 }
 
 // result[t, h] = sum_j w[t, j] * down[inv[t*k + j], h], j ascending, fp32.
+// Grid: x = token (up to 2^31 - 1), y = 256-column block of H.
 __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ down, int dtype,
                                                       const int32_t* __restrict__ inv,
                                                       const void* __restrict__ w, int wdtype,
                                                       int top_k, int H, int n_rows,
                                                       void* __restrict__ out) {
-  const int t = blockIdx.y;
-  const int h = blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = blockIdx.x;
+  const int h = blockIdx.y * blockDim.x + threadIdx.x;
   if (h >= H) return;
   float acc = 0.f;
   for (int j = 0; j < top_k; ++j) {
@@ -186,6 +187,8 @@ extern "C" int exq_combine(const void* down_out, int dtype, const int64_t* sort_
                   n_active <= INT32_MAX && hidden_size > 0,
               "exq_combine: n_active (%lld) must equal n_tokens*top_k (%lld)",
               (long long)n_active, (long long)(n_tokens * top_k));
+  EXQ_REQUIRE(cdiv(hidden_size, 256) <= 65535, "exq_combine: hidden_size=%lld too large",
+              (long long)hidden_size);
   if (n_tokens == 0) return EXQ_SUCCESS;
   if (workspace_bytes < exq_combine_workspace_size(n_active))
     return set_error(EXQ_ERROR_WORKSPACE_TOO_SMALL, "exq_combine: workspace %zu < %zu bytes",
@@ -198,7 +201,7 @@ extern "C" int exq_combine(const void* down_out, int dtype, const int64_t* sort_
                      sort_order, (int)n_active, inv);
   int st = check_launch("inverse_perm_kernel");
   if (st) return st;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)cdiv(hidden_size, 256), (unsigned)n_tokens),
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)n_tokens, (unsigned)cdiv(hidden_size, 256)),
                      dim3(256), 0, s, down_out, dtype, inv, router_weights, weights_dtype,
                      (int)top_k, (int)hidden_size, (int)n_active, result);
   return check_launch("combine_kernel");
