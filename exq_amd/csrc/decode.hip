@@ -68,6 +68,10 @@ constexpr int MAX_SLOTS = 1024;    // T * (k + n_shared)
 constexpr int MAX_BM_WORDS = 32;   // active-expert bitmap: E + shared <= 1024
 constexpr int kCombineLaunchMinT = 32;     // down combine: own launch from this batch on,
 constexpr int kCombineLaunchMinSplit = 4;  // or from this many k-splits on; else in-kernel
+// The down projection by output rows (decode_down_t1_kernel) up to this batch
+// (measured, µs per layer, rows / tiles: Qwen3 T=1 15.2 / 19.5, T=2 20.1 /
+// 22.6, T=3 24.1 / 23.6; OLMoE T=2 21.2 / 24.5, T=4 28.6 / 26.3).
+constexpr int kRowsDownMaxT = 2;
 
 // Output rows of a down unit: 64 (four row sets), 32 when a pass holds two
 // or four 16-row tiles (register budget of the accumulators).
@@ -1238,6 +1242,150 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(LayerArgs a) {
   *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.H + h) = o;
 }
 
+// ---- few tokens: the down projection by output rows ------------------------
+// For a few tokens (T * (k + shared) <= T1_MAX_SLOTS) a work-group owns
+// T1_ROWS output rows across all of the batch's routed slots and sums each
+// token's slots itself: no fp32 partial rows, no counters, no combine tail
+// (at T = 1 that tail is most of the down kernel's time).  A slot's weights
+// are read per slot, so an expert routed by several tokens is read again (from
+// L2).  Half-wave hw of slot group s0 takes slot s0 + hw (token s / kp); its
+// 32 lanes take the 32-k chunks c = lane, lane + 32, ... of the slot's `mid`
+// row (stored in INT4 pairing order: pairs (k, k + 4) of each
+// 8-group) and, for each of the rows, the matching 16 packed bytes.  Nibbles
+// become exact 16-bit floats base + n with one v_and_or_b32 per pair, in the
+// same pairing order, and v_dot2 multiplies and adds them in fp32; the
+// constant base is removed once per chunk (a v_dot2 of `mid` against ones),
+// and the fp16 group scale multiplies the chunk's sum.  Each half-wave's 32
+// lane sums are folded in a fixed order (DPP inside 16-lane rows, then the
+// two rows), and each token's weighted slot rows are summed in ascending slot
+// order: the result does not depend on scheduling.
+constexpr int T1_ROWS = 4;        // output rows per work-group
+constexpr int T1_MAX_SLOTS = 64;  // T * (k + shared)
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+template <bool BF>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                           __builtin_bit_cast(bf16x2_t, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b),
+                                  c, false);
+}
+
+template <bool BF>
+__global__ void __launch_bounds__(256) decode_down_t1_kernel(LayerArgs a) {
+  constexpr int R = T1_ROWS;
+  __shared__ float red[T1_MAX_SLOTS][R];
+  const int h0 = blockIdx.x * R;
+  const int lane = threadIdx.x & 63, hw = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int C = a.I >> 5;                  // 32-k chunks per row
+  const int gch = 4 << a.gshift;           // chunks per scale group
+  const int ng = a.I >> (7 + a.gshift);    // scale groups per row
+  const int rowb = a.I >> 1;               // packed bytes per row
+  const uint32_t dq_mask = 0x000F000Fu;
+  const uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
+  const uint32_t ones = BF ? 0x3F803F80u : 0x3C003C00u;
+  const float base = BF ? 136.f : 1032.f;  // base + 8: (base + n) - (base + 8) = n - 8
+  const int n_slots = a.T * a.kp;
+  const __amdgpu_buffer_rsrc_t mid_r = make_rsrc(a.mid, (int64_t)n_slots * a.I * 2);
+  for (int s0 = 0; s0 < n_slots; s0 += 8) {
+    const int s = s0 + hw;
+    int e = -1;
+    float wt = 0.f;
+    if (s < n_slots) {
+      const int t = s / a.kp, j = s - t * a.kp;
+      if (j < a.k) {
+        const int64_t id = load_index(a.ids, a.ids_dtype, (int64_t)t * a.k + j);
+        if (id >= 0 && id < a.E) {
+          e = (int)id;
+          wt = load_as_f32(a.topk_w, a.w_dtype, (int64_t)t * a.k + j);
+        }
+      } else {
+        e = a.E + (j - a.k);  // shared expert, weight 1
+        wt = 1.f;
+      }
+    }
+    float part[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[r] = 0.f;
+    if (e >= 0) {
+      const int64_t row0 = (int64_t)(a.index ? a.index[e] : e) * a.H + h0;
+      const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w2.i4 + row0 * rowb, (int64_t)R * rowb);
+      const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.w2.i4_scales + row0 * ng, (int64_t)R * ng * 2);
+      for (int c = l; c < C; c += 32) {
+        uint4 m[4], w[R];
+        uint32_t sc[R];
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          m[d] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              mid_r, (s * a.I + c * 32 + d * 8) * 2, 0, 0));
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          w[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              wr, r * rowb + c * 16, 0, 0));
+          sc[r] = __builtin_amdgcn_raw_buffer_load_b16(sr, (r * ng + c / gch) * 2, 0, 0);
+        }
+        float msum = 0.f;  // the chunk's sum of mid values
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          msum = dot2<BF>(m[d].x, ones, msum);
+          msum = dot2<BF>(m[d].y, ones, msum);
+          msum = dot2<BF>(m[d].z, ones, msum);
+          msum = dot2<BF>(m[d].w, ones, msum);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float acc = 0.f;
+          const uint32_t pw[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {  // word d: k = 8d .. 8d + 7; pair q = (k_q, k_q+4)
+            const uint32_t p = pw[d];
+            acc = dot2<BF>((p & dq_mask) | dq_magic, m[d].x, acc);
+            acc = dot2<BF>(((p >> 4) & dq_mask) | dq_magic, m[d].y, acc);
+            acc = dot2<BF>(((p >> 8) & dq_mask) | dq_magic, m[d].z, acc);
+            acc = dot2<BF>(((p >> 12) & dq_mask) | dq_magic, m[d].w, acc);
+          }
+          part[r] += f16_bits_to_f32(sc[r]) * (acc - base * msum);
+        }
+      }
+    }
+    // fold each half-wave's 32 lanes: DPP sums inside 16-lane rows, then the rows
+    const float w_lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), 0));
+    const float w_hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wt), 32));
+    const int sw = s0 + 2 * (threadIdx.x >> 6);  // this wave's first slot
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float v = part[r];
+      v += dpp_f32<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+      v += dpp_f32<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+      v += dpp_f32<0x124>(v);  // row_ror 4
+      v += dpp_f32<0x128>(v);  // row_ror 8
+      const int vi = __builtin_bit_cast(int, v);
+      const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+      const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+                       __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+      if (lane == 0) {
+        if (sw < n_slots) red[sw][r] = w_lo * lo;
+        if (sw + 1 < n_slots) red[sw + 1][r] = w_hi * hi;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < a.T * R) {  // out[t, row] = sum over the token's slots, ascending
+    const int t = threadIdx.x / R, r = threadIdx.x - t * R;
+    float o = 0.f;
+    for (int j = 0; j < a.kp; ++j) o += red[t * a.kp + j][r];
+    a.out[(int64_t)t * a.H + h0 + r] = (uint16_t)to_act_bits<BF>(o);
+  }
+}
+
 typedef void (*decode_kernel_t)(LayerArgs);
 
 template <bool BF, int PH>
@@ -1335,6 +1483,17 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   // need repeated ids; the work-groups then stride over the extra units).
   const int64_t max_tiles = d.T <= 16 ? max_active : max_active + ((int64_t)d.T * d.kp + 15) / 16;
   for (int ph = 0; ph < 2; ++ph) {
+    const hipEvent_t* ev = stage_events();
+    if (ph == 1 && d.T <= kRowsDownMaxT && !mixed && d.kp >= 4 && d.T * d.kp <= T1_MAX_SLOTS) {
+      // few tokens: the down projection by output rows, summed in-kernel
+      const dim3 g1((unsigned)(d.H / T1_ROWS));
+      const auto k1 = d.bf ? decode_down_t1_kernel<true> : decode_down_t1_kernel<false>;
+      if (ev)
+        hipExtLaunchKernelGGL(k1, g1, dim3(256), 0, s, ev[2], ev[3], 0, a);
+      else
+        hipLaunchKernelGGL(k1, g1, dim3(256), 0, s, a);
+      return check_launch("decode_down_t1_kernel");
+    }
     // per-wave weight slices / partial tiles, then the per-expert row counts
     const size_t lds = (size_t)DW * WAVE_LDS + (((size_t)(d.Ep + 1) / 2 * 4 + 15) & ~(size_t)15);
     if (ph == 1) {
@@ -1388,7 +1547,6 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     const dim3 g((unsigned)(grid > 0 ? grid : 1));
     // stage events: start / stop of exactly this kernel (the down stage ends
     // after the combine launch when there is one)
-    const hipEvent_t* ev = stage_events();
     const bool tail = ph == 1 && !a.combine;
     if (ev)
       hipExtLaunchKernelGGL(kern, g, dim3(DNT), klds, s, ev[2 * ph],

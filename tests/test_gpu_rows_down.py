@@ -1,0 +1,62 @@
+"""The decode layer's down projection by output rows (batches of one or two
+tokens, k + shared >= 4, T * (k + shared) <= 64), against the oracle:
+several top-k (up to the 64-slot limit), dropped ids, bf16 and f16
+activations, group sizes 128 and 256, an intermediate size whose 32-k chunks
+do not divide evenly over 32 lanes (I = 1280: 40 chunks), and top-k below
+the kernel's minimum (which runs the tiled down kernel).  Each layer is also
+computed twice and compared bitwise.  Tolerance: relative L2 <= 0.5 %."""
+import numpy as np
+import pytest
+import torch
+
+from exq_amd import synth
+from oracle import moe, quant
+from tests._helpers import assert_close_rel, banner
+
+pytestmark = pytest.mark.gpu
+
+TOL = 5e-3
+
+# (E, H, I, group size, k, T, activation dtype, drop fraction)
+CASES = [
+    (128, 2048, 768, 128, 8, 1, torch.bfloat16, 0.0),    # Qwen3 layer shape
+    (64, 2048, 1024, 128, 8, 2, torch.bfloat16, 0.0),    # OLMoE layer shape
+    (16, 256, 256, 128, 4, 1, torch.float16, 0.0),       # the minimum top-k
+    (16, 256, 256, 128, 3, 1, torch.bfloat16, 0.0),      # below it: tiled down kernel
+    (40, 512, 1280, 128, 6, 2, torch.bfloat16, 0.2),     # 40 chunks, dropped ids
+    (40, 512, 1280, 256, 6, 1, torch.float16, 0.0),      # group size 256
+    (96, 256, 384, 128, 32, 2, torch.bfloat16, 0.1),     # 64 slots, the limit
+    (128, 256, 512, 128, 32, 1, torch.float16, 0.5),     # half the slots dropped
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_rows_down(case, device):
+    from exq_amd.kernels import fused_experts, pack_experts_int4
+    E, H, I, g, k, T, act, drop = CASES[case]
+    banner(f"rows down E={E} H={H} I={I} g={g} k={k} T={T} {act} drop={drop}")
+    rng = np.random.default_rng(900 + case)
+    w13, w2 = synth.expert_weights_gpu(E, I, H, 900 + case, device)
+    p13, s13 = pack_experts_int4(w13, group_size=g)
+    p2, s2 = pack_experts_int4(w2, group_size=g)
+    del w13, w2
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    if drop:
+        ids[rng.random(ids.shape) < drop] = -1
+    w = rng.random((T, k)).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(act).to(device)
+    tid, tw = torch.from_numpy(ids).to(device), torch.from_numpy(w).to(device)
+    out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+    again = fused_experts(x, p13, s13, p2, s2, tw, tid)
+    assert torch.equal(out, again), "rows-down layer is not bitwise repeatable"
+    used = np.unique(ids[ids >= 0])
+    d13 = np.zeros((E, 2 * I, H), np.float32)
+    d2 = np.zeros((E, H, I), np.float32)
+    for e in used:
+        d13[e] = quant.dequant_int4(p13[e].cpu().numpy(), s13[e].cpu().numpy())
+        d2[e] = quant.dequant_int4(p2[e].cpu().numpy(), s2[e].cpu().numpy())
+    ref = moe.moe_layer(x.float().cpu().numpy(), d13, d2, ids, w)
+    if not used.size:
+        assert torch.count_nonzero(out) == 0
+        return
+    assert_close_rel(out, ref, TOL, f"rows down case {case}")
