@@ -69,9 +69,13 @@ constexpr int MAX_BM_WORDS = 32;   // active-expert bitmap: E + shared <= 1024
 constexpr int kCombineLaunchMinT = 32;     // down combine: own launch from this batch on,
 constexpr int kCombineLaunchMinSplit = 4;  // or from this many k-splits on; else in-kernel
 // The down projection by output rows (decode_down_t1_kernel) up to this batch
-// (measured, µs per layer, rows / tiles: Qwen3 T=1 15.2 / 19.5, T=2 20.1 /
-// 22.6, T=3 24.1 / 23.6; OLMoE T=2 21.2 / 24.5, T=4 28.6 / 26.3).
+// (measured on 48 streamed Qwen3 layers, µs per layer, rows / tiled down:
+// T=1 15.2 / 19.5, T=2 20.1 / 22.6, T=3 24.1 / 23.6, T=4 28.3 / 25.2).
 constexpr int kRowsDownMaxT = 2;
+// The gate/up projection by output rows (decode_gateup_rows_kernel) up to this
+// batch (same layers, with the rows down kernel, rows / tiled gate/up: T=1
+// 14.5 / 15.2, T=2 21.0 / 20.1).
+constexpr int kRowsGateUpMaxT = 1;
 
 // Output rows of a down unit: 64 (four row sets), 32 when a pass holds two
 // or four 16-row tiles (register budget of the accumulators).
@@ -1278,6 +1282,113 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                   c, false);
 }
 
+// The gate/up projection for the same batches, by output rows: work-group
+// (x, y) takes routed slot y and the GU_PAIRS (gate j, up I + j) row pairs
+// j = x * GU_PAIRS + hw, one per half-wave.  A slot's expert is one load of
+// its id (no active-expert list is needed).  Lanes take the 32-k chunks
+// c = lane, lane + 32, ... of the token's row of x, permuted into the nibbles'
+// pairing order, and dot2 both rows' dequantised nibbles against it (as in
+// decode_down_t1_kernel); the folded gate and up sums give SiLU(g) * u, stored
+// in `mid` in INT4 pairing order.
+constexpr int GU_PAIRS = 8;
+
+template <bool BF, int NCH>  // NCH >= ceil(H / 1024): 32-k chunks per lane, all loads issued first
+__global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
+  const int s = blockIdx.y;  // routed slot t * kp + j
+  const int t = s / a.kp, js = s - t * a.kp;
+  int e;
+  if (js < a.k) {
+    const int64_t id = load_index(a.ids, a.ids_dtype, (int64_t)t * a.k + js);
+    if (id < 0 || id >= a.E) return;  // dropped slot: no mid row (the down kernel skips it)
+    e = (int)id;
+  } else {
+    e = a.E + (js - a.k);  // shared expert
+  }
+  const int lane = threadIdx.x & 63, hw = threadIdx.x >> 5, l = threadIdx.x & 31;
+  const int j = blockIdx.x * GU_PAIRS + hw;  // gate row j, up row I + j
+  const int C = a.H >> 5;
+  const int gch = 4 << a.gshift;
+  const int ng = a.H >> (7 + a.gshift);
+  const int rowb = a.H >> 1;
+  const uint32_t dq_mask = 0x000F000Fu;
+  const uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
+  const uint32_t ones = BF ? 0x3F803F80u : 0x3C003C00u;
+  const float base = BF ? 136.f : 1032.f;
+  const int64_t rg = (int64_t)(a.index ? a.index[e] : e) * 2 * a.I + j;  // gate row
+  const int64_t ru = rg + a.I;                                            // up row
+  const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.w13.i4 + rg * rowb, rowb);
+  const __amdgpu_buffer_rsrc_t ur = make_rsrc(a.w13.i4 + ru * rowb, rowb);
+  const __amdgpu_buffer_rsrc_t gsr = make_rsrc(a.w13.i4_scales + rg * ng, (int64_t)ng * 2);
+  const __amdgpu_buffer_rsrc_t usr = make_rsrc(a.w13.i4_scales + ru * ng, (int64_t)ng * 2);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x + (int64_t)t * a.H, (int64_t)a.H * 2);
+  uint4 xv[NCH][4], gw[NCH], uw[NCH];
+  uint32_t gs[NCH], us[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {  // chunk c = l + 32 i; past C the loads return zero
+    const int c = l + 32 * i;
+    const bool ok = c < C;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      xv[i][d] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? (c * 32 + d * 8) * 2 : OOB_OFF, 0, 0));
+    gw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(gr, ok ? c * 16 : OOB_OFF, 0, 0));
+    uw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ur, ok ? c * 16 : OOB_OFF, 0, 0));
+    gs[i] = __builtin_amdgcn_raw_buffer_load_b16(gsr, ok ? (c / gch) * 2 : OOB_OFF, 0, 0);
+    us[i] = __builtin_amdgcn_raw_buffer_load_b16(usr, ok ? (c / gch) * 2 : OOB_OFF, 0, 0);
+  }
+  float g = 0.f, u = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    float xsum = 0.f;  // the chunk's sum of x (any order)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      xsum = dot2<BF>(xv[i][d].x, ones, xsum);
+      xsum = dot2<BF>(xv[i][d].y, ones, xsum);
+      xsum = dot2<BF>(xv[i][d].z, ones, xsum);
+      xsum = dot2<BF>(xv[i][d].w, ones, xsum);
+      xv[i][d] = dperm(xv[i][d]);  // pairs (k_q, k_q+4), the nibbles' order
+    }
+    float ag = 0.f, au = 0.f;
+    const uint32_t pg[4] = {gw[i].x, gw[i].y, gw[i].z, gw[i].w};
+    const uint32_t pu[4] = {uw[i].x, uw[i].y, uw[i].z, uw[i].w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      ag = dot2<BF>((pg[d] & dq_mask) | dq_magic, xv[i][d].x, ag);
+      ag = dot2<BF>(((pg[d] >> 4) & dq_mask) | dq_magic, xv[i][d].y, ag);
+      ag = dot2<BF>(((pg[d] >> 8) & dq_mask) | dq_magic, xv[i][d].z, ag);
+      ag = dot2<BF>(((pg[d] >> 12) & dq_mask) | dq_magic, xv[i][d].w, ag);
+      au = dot2<BF>((pu[d] & dq_mask) | dq_magic, xv[i][d].x, au);
+      au = dot2<BF>(((pu[d] >> 4) & dq_mask) | dq_magic, xv[i][d].y, au);
+      au = dot2<BF>(((pu[d] >> 8) & dq_mask) | dq_magic, xv[i][d].z, au);
+      au = dot2<BF>(((pu[d] >> 12) & dq_mask) | dq_magic, xv[i][d].w, au);
+    }
+    // a chunk past C read zeros: its sums and scale are zero
+    g += f16_bits_to_f32(gs[i]) * (ag - base * xsum);
+    u += f16_bits_to_f32(us[i]) * (au - base * xsum);
+  }
+  // fold each half-wave's 32 lanes (fixed order), as decode_down_t1_kernel
+  auto fold = [&](float v, float& lo, float& hi) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x124>(v);
+    v += dpp_f32<0x128>(v);
+    const int vi = __builtin_bit_cast(int, v);
+    lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 0)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 16));
+    hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 32)) +
+         __builtin_bit_cast(float, __builtin_amdgcn_readlane(vi, 48));
+  };
+  float g_lo, g_hi, u_lo, u_hi;
+  fold(g, g_lo, g_hi);
+  fold(u, u_lo, u_hi);
+  if (lane == 0) {  // this wave's two row pairs j0 = j (lo) and j0 + 1 (hi)
+    const int j0 = blockIdx.x * GU_PAIRS + 2 * (threadIdx.x >> 6);
+    uint16_t* mrow = a.mid + (int64_t)s * a.I;
+    mrow[(j0 & ~7) + pair_pos(j0 & 7)] = (uint16_t)to_act_bits<BF>(silu_f32(g_lo) * u_lo);
+    mrow[((j0 + 1) & ~7) + pair_pos((j0 + 1) & 7)] = (uint16_t)to_act_bits<BF>(silu_f32(g_hi) * u_hi);
+  }
+}
+
 template <bool BF>
 __global__ void __launch_bounds__(256) decode_down_t1_kernel(LayerArgs a) {
   constexpr int R = T1_ROWS;
@@ -1482,9 +1593,26 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   // grid is sized for one tile per expert up to T = 16 (more tiles there
   // need repeated ids; the work-groups then stride over the extra units).
   const int64_t max_tiles = d.T <= 16 ? max_active : max_active + ((int64_t)d.T * d.kp + 15) / 16;
+  const bool rows = d.T <= kRowsDownMaxT && !mixed && d.kp >= 4 && d.T * d.kp <= T1_MAX_SLOTS;
+  const bool rows_gu = rows && d.T <= kRowsGateUpMaxT && d.I % GU_PAIRS == 0 && d.H <= 4096;
   for (int ph = 0; ph < 2; ++ph) {
     const hipEvent_t* ev = stage_events();
-    if (ph == 1 && d.T <= kRowsDownMaxT && !mixed && d.kp >= 4 && d.T * d.kp <= T1_MAX_SLOTS) {
+    if (ph == 0 && rows_gu) {
+      // few tokens: the gate/up projection by output rows
+      const dim3 g0((unsigned)(d.I / GU_PAIRS), (unsigned)(d.T * d.kp));
+      const int nch = (d.H / 32 + 31) / 32;  // chunks per lane
+      const auto k0 = nch <= 1 ? (d.bf ? decode_gateup_rows_kernel<true, 1> : decode_gateup_rows_kernel<false, 1>)
+                    : nch <= 2 ? (d.bf ? decode_gateup_rows_kernel<true, 2> : decode_gateup_rows_kernel<false, 2>)
+                               : (d.bf ? decode_gateup_rows_kernel<true, 4> : decode_gateup_rows_kernel<false, 4>);
+      if (ev)
+        hipExtLaunchKernelGGL(k0, g0, dim3(256), 0, s, ev[0], ev[1], 0, a);
+      else
+        hipLaunchKernelGGL(k0, g0, dim3(256), 0, s, a);
+      const int st = check_launch("decode_gateup_rows_kernel");
+      if (st) return st;
+      continue;
+    }
+    if (ph == 1 && rows) {
       // few tokens: the down projection by output rows, summed in-kernel
       const dim3 g1((unsigned)(d.H / T1_ROWS));
       const auto k1 = d.bf ? decode_down_t1_kernel<true> : decode_down_t1_kernel<false>;
