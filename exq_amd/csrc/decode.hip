@@ -1389,7 +1389,11 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
   }
 }
 
-template <bool BF>
+// MIXED: the bank's tiers per expert (INT4 as above; BF16 rows are multiplied
+// as stored, against `mid` put back in natural order; INT8 bytes become exact
+// 16-bit pairs and the row's fp16 scale multiplies the sum).  NCH: 32-k chunks
+// per lane (all of a lane's loads are issued before its arithmetic).
+template <bool BF, bool MIXED, int NCH>
 __global__ void __launch_bounds__(256) decode_down_t1_kernel(LayerArgs a) {
   constexpr int R = T1_ROWS;
   __shared__ float red[T1_MAX_SLOTS][R];
@@ -1398,7 +1402,7 @@ __global__ void __launch_bounds__(256) decode_down_t1_kernel(LayerArgs a) {
   const int C = a.I >> 5;                  // 32-k chunks per row
   const int gch = 4 << a.gshift;           // chunks per scale group
   const int ng = a.I >> (7 + a.gshift);    // scale groups per row
-  const int rowb = a.I >> 1;               // packed bytes per row
+  const int rowb = a.I >> 1;               // packed bytes per INT4 row
   const uint32_t dq_mask = 0x000F000Fu;
   const uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
   const uint32_t ones = BF ? 0x3F803F80u : 0x3C003C00u;
@@ -1426,43 +1430,119 @@ __global__ void __launch_bounds__(256) decode_down_t1_kernel(LayerArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) part[r] = 0.f;
     if (e >= 0) {
-      const int64_t row0 = (int64_t)(a.index ? a.index[e] : e) * a.H + h0;
-      const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w2.i4 + row0 * rowb, (int64_t)R * rowb);
-      const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.w2.i4_scales + row0 * ng, (int64_t)R * ng * 2);
-      for (int c = l; c < C; c += 32) {
-        uint4 m[4], w[R];
-        uint32_t sc[R];
+      const int idx = a.index ? a.index[e] : e;  // row of the expert in its tier's bank
+      const int tier = MIXED ? (int)a.tier[e] : 2;
+      const int64_t row0 = (int64_t)idx * a.H + h0;
+      uint4 m[NCH][4];  // mid chunks c = l + 32 i (zeros past C)
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int c = l + 32 * i;
 #pragma unroll
         for (int d = 0; d < 4; ++d)
-          m[d] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              mid_r, (s * a.I + c * 32 + d * 8) * 2, 0, 0));
+          m[i][d] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 mid_r, c < C ? (s * a.I + c * 32 + d * 8) * 2 : OOB_OFF, 0, 0));
+      }
+      if (tier == 2) {
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w2.i4 + row0 * rowb, (int64_t)R * rowb);
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.w2.i4_scales + row0 * ng, (int64_t)R * ng * 2);
+        uint4 w[NCH][R];
+        uint32_t sc[NCH][R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          w[r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                              wr, r * rowb + c * 16, 0, 0));
-          sc[r] = __builtin_amdgcn_raw_buffer_load_b16(sr, (r * ng + c / gch) * 2, 0, 0);
-        }
-        float msum = 0.f;  // the chunk's sum of mid values
+        for (int i = 0; i < NCH; ++i) {
+          const int c = l + 32 * i;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          msum = dot2<BF>(m[d].x, ones, msum);
-          msum = dot2<BF>(m[d].y, ones, msum);
-          msum = dot2<BF>(m[d].z, ones, msum);
-          msum = dot2<BF>(m[d].w, ones, msum);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          float acc = 0.f;
-          const uint32_t pw[4] = {w[r].x, w[r].y, w[r].z, w[r].w};
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {  // word d: k = 8d .. 8d + 7; pair q = (k_q, k_q+4)
-            const uint32_t p = pw[d];
-            acc = dot2<BF>((p & dq_mask) | dq_magic, m[d].x, acc);
-            acc = dot2<BF>(((p >> 4) & dq_mask) | dq_magic, m[d].y, acc);
-            acc = dot2<BF>(((p >> 8) & dq_mask) | dq_magic, m[d].z, acc);
-            acc = dot2<BF>(((p >> 12) & dq_mask) | dq_magic, m[d].w, acc);
+          for (int r = 0; r < R; ++r) {
+            w[i][r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    wr, c < C ? r * rowb + c * 16 : OOB_OFF, 0, 0));
+            sc[i][r] = __builtin_amdgcn_raw_buffer_load_b16(sr, c < C ? (r * ng + c / gch) * 2 : OOB_OFF, 0, 0);
           }
-          part[r] += f16_bits_to_f32(sc[r]) * (acc - base * msum);
+        }
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+          float msum = 0.f;  // the chunk's sum of mid values
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            msum = dot2<BF>(m[i][d].x, ones, msum);
+            msum = dot2<BF>(m[i][d].y, ones, msum);
+            msum = dot2<BF>(m[i][d].z, ones, msum);
+            msum = dot2<BF>(m[i][d].w, ones, msum);
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float acc = 0.f;
+            const uint32_t pw[4] = {w[i][r].x, w[i][r].y, w[i][r].z, w[i][r].w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {  // word d: k = 8d .. 8d + 7; pair q = (k_q, k_q+4)
+              const uint32_t p = pw[d];
+              acc = dot2<BF>((p & dq_mask) | dq_magic, m[i][d].x, acc);
+              acc = dot2<BF>(((p >> 4) & dq_mask) | dq_magic, m[i][d].y, acc);
+              acc = dot2<BF>(((p >> 8) & dq_mask) | dq_magic, m[i][d].z, acc);
+              acc = dot2<BF>(((p >> 12) & dq_mask) | dq_magic, m[i][d].w, acc);
+            }
+            // a chunk past C read zeros: its scale is zero
+            part[r] += f16_bits_to_f32(sc[i][r]) * (acc - base * msum);
+          }
+        }
+      } else if constexpr (MIXED) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) m[i][d] = dperm_inv(m[i][d]);  // natural k order
+        if (tier == 0) {  // 16-bit weights as stored: rows of I values
+          const __amdgpu_buffer_rsrc_t wr =
+              make_rsrc(a.w2.bf16 + row0 * a.I, (int64_t)R * a.I * 2);
+#pragma unroll
+          for (int i = 0; i < NCH; ++i) {
+            const int c = l + 32 * i;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              float acc = 0.f;
+#pragma unroll
+              for (int d = 0; d < 4; ++d) {
+                const uint4 wv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                    wr, c < C ? (r * a.I + c * 32 + d * 8) * 2 : OOB_OFF, 0, 0));
+                acc = dot2<BF>(wv.x, m[i][d].x, acc);
+                acc = dot2<BF>(wv.y, m[i][d].y, acc);
+                acc = dot2<BF>(wv.z, m[i][d].z, acc);
+                acc = dot2<BF>(wv.w, m[i][d].w, acc);
+              }
+              part[r] += acc;
+            }
+          }
+        } else {  // INT8 rows of I bytes, fp16 scale per row
+          const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w2.i8 + row0 * a.I, (int64_t)R * a.I);
+          auto pair16 = [&](uint32_t wd, int b) {  // bytes b, b+1 of wd -> exact 16-bit pair
+            const float lo = (float)(int8_t)(wd >> (8 * b));
+            const float hi = (float)(int8_t)(wd >> (8 * b + 8));
+            if constexpr (BF)
+              return (__builtin_bit_cast(uint32_t, lo) >> 16) |
+                     (__builtin_bit_cast(uint32_t, hi) & 0xffff0000u);
+            else
+              return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+          };
+#pragma unroll
+          for (int i = 0; i < NCH; ++i) {
+            const int c = l + 32 * i;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              float acc = 0.f;
+#pragma unroll
+              for (int h = 0; h < 2; ++h) {  // 16 bytes: k = 16 h .. 16 h + 15
+                const uint4 wv = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                    wr, c < C ? r * a.I + c * 32 + h * 16 : OOB_OFF, 0, 0));
+                const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+                const uint4& m0 = m[i][2 * h];
+                const uint4& m1 = m[i][2 * h + 1];
+                const uint32_t mm[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  acc = dot2<BF>(pair16(ww[q], 0), mm[2 * q], acc);
+                  acc = dot2<BF>(pair16(ww[q], 2), mm[2 * q + 1], acc);
+                }
+              }
+              part[r] += f16_bits_to_f32(a.w2.i8_scales[row0 + r]) * acc;
+            }
+          }
         }
       }
     }
@@ -1593,8 +1673,8 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   // grid is sized for one tile per expert up to T = 16 (more tiles there
   // need repeated ids; the work-groups then stride over the extra units).
   const int64_t max_tiles = d.T <= 16 ? max_active : max_active + ((int64_t)d.T * d.kp + 15) / 16;
-  const bool rows = d.T <= kRowsDownMaxT && !mixed && d.kp >= 4 && d.T * d.kp <= T1_MAX_SLOTS;
-  const bool rows_gu = rows && d.T <= kRowsGateUpMaxT && d.I % GU_PAIRS == 0 && d.H <= 4096;
+  const bool rows = d.T <= kRowsDownMaxT && d.kp >= 4 && d.T * d.kp <= T1_MAX_SLOTS && d.I <= 2048;
+  const bool rows_gu = rows && !mixed && d.T <= kRowsGateUpMaxT && d.I % GU_PAIRS == 0 && d.H <= 4096;
   for (int ph = 0; ph < 2; ++ph) {
     const hipEvent_t* ev = stage_events();
     if (ph == 0 && rows_gu) {
@@ -1615,7 +1695,14 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     if (ph == 1 && rows) {
       // few tokens: the down projection by output rows, summed in-kernel
       const dim3 g1((unsigned)(d.H / T1_ROWS));
-      const auto k1 = d.bf ? decode_down_t1_kernel<true> : decode_down_t1_kernel<false>;
+      const int nch = (d.I / 32 + 31) / 32;  // chunks per lane
+      decode_kernel_t k1;
+      if (mixed)
+        k1 = nch <= 1 ? (d.bf ? decode_down_t1_kernel<true, true, 1> : decode_down_t1_kernel<false, true, 1>)
+                      : (d.bf ? decode_down_t1_kernel<true, true, 2> : decode_down_t1_kernel<false, true, 2>);
+      else
+        k1 = nch <= 1 ? (d.bf ? decode_down_t1_kernel<true, false, 1> : decode_down_t1_kernel<false, false, 1>)
+                      : (d.bf ? decode_down_t1_kernel<true, false, 2> : decode_down_t1_kernel<false, false, 2>);
       if (ev)
         hipExtLaunchKernelGGL(k1, g1, dim3(256), 0, s, ev[2], ev[3], 0, a);
       else

@@ -60,3 +60,35 @@ def test_rows_down(case, device):
         assert torch.count_nonzero(out) == 0
         return
     assert_close_rel(out, ref, TOL, f"rows down case {case}")
+
+
+# mixed banks: (E, H, I, k, T, n_shared, tiers (None = from synth.mixed_tiers), act)
+MIXED = [
+    (16, 512, 256, 4, 1, 0, [1] * 8 + [2] * 4 + [0] * 4, torch.bfloat16),   # mostly INT8
+    (16, 512, 1280, 6, 2, 2, None, torch.bfloat16),                         # shared experts, 40 chunks
+    (64, 2048, 1408, 6, 1, 2, [2] * 64, torch.bfloat16),                    # DeepSeek-V2-Lite shape
+    (16, 512, 256, 5, 2, 1, [0] * 6 + [1] * 5 + [2] * 5, torch.float16),
+]
+
+
+@pytest.mark.parametrize("case", range(len(MIXED)))
+def test_rows_down_mixed(case, device):
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    from tests.test_gpu_mixed import _oracle
+    E, H, I, k, T, S, tiers, act = MIXED[case]
+    banner(f"rows down mixed E={E} H={H} I={I} k={k} T={T} shared={S} {act}")
+    rng = np.random.default_rng(950 + case)
+    w13, w2 = synth.expert_weights_gpu(E, I, H, 950 + case, device)
+    sh13 = sh2 = None
+    if S:
+        sh13, sh2 = synth.expert_weights_gpu(S, I, H, 960 + case, device)
+    tiers = tiers if tiers is not None else synth.mixed_tiers(E, 950 + case)
+    bank = MixedExpertBank.from_weights(w13, w2, tiers, act_dtype=act, shared_w13=sh13,
+                                        shared_w2=sh2, shared_tier=0)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    w = rng.random((T, k)).astype(np.float32)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(act).to(device)
+    tid, tw = torch.from_numpy(ids).to(device), torch.from_numpy(w).to(device)
+    out = fused_experts_mixed(x, bank, tw, tid)
+    assert torch.equal(out, fused_experts_mixed(x, bank, tw, tid))
+    assert_close_rel(out, _oracle(bank, x, ids, w), TOL, f"rows down mixed case {case}")
