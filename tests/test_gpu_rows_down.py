@@ -1,9 +1,11 @@
 """The decode layer's down projection by output rows (batches of one or two
 tokens, k + shared >= 4, T * (k + shared) <= 64), against the oracle:
 several top-k (up to the 64-slot limit), dropped ids, bf16 and f16
-activations, group sizes 128 and 256, an intermediate size whose 32-k chunks
-do not divide evenly over 32 lanes (I = 1280: 40 chunks), and top-k below
-the kernel's minimum (which runs the tiled down kernel).  Each layer is also
+activations, int32 / int64 ids and f32 / bf16 / f16 router weights, group
+sizes 128 and 256, an intermediate size whose 32-k chunks do not divide
+evenly over 32 lanes (I = 1280: 40 chunks), mixed BF16 / INT8 / INT4 banks
+with shared experts, and top-k below the kernel's minimum (which runs the
+tiled down kernel).  Each layer is also
 computed twice and compared bitwise.  Tolerance: relative L2 <= 0.5 %."""
 import numpy as np
 import pytest
@@ -45,7 +47,12 @@ def test_rows_down(case, device):
         ids[rng.random(ids.shape) < drop] = -1
     w = rng.random((T, k)).astype(np.float32)
     x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(act).to(device)
-    tid, tw = torch.from_numpy(ids).to(device), torch.from_numpy(w).to(device)
+    # id and router-weight dtypes vary over the cases (the kernel reads either)
+    ids_dt = (torch.int64, torch.int32)[case % 2]
+    w_dt = (torch.float32, torch.bfloat16, torch.float16)[case % 3]
+    tid = torch.from_numpy(ids).to(ids_dt).to(device)
+    tw = torch.from_numpy(w).to(w_dt).to(device)
+    w = tw.float().cpu().numpy()  # the weights as the kernel reads them
     out = fused_experts(x, p13, s13, p2, s2, tw, tid)
     again = fused_experts(x, p13, s13, p2, s2, tw, tid)
     assert torch.equal(out, again), "rows-down layer is not bitwise repeatable"
