@@ -68,7 +68,7 @@ constexpr int MAX_SLOTS = 1024;    // T * (k + n_shared)
 constexpr int MAX_BM_WORDS = 32;   // active-expert bitmap: E + shared <= 1024
 constexpr int kCombineLaunchMinT = 32;     // down combine: own launch from this batch on,
 constexpr int kCombineLaunchMinSplit = 4;  // or from this many k-splits on; else in-kernel
-// The down projection by output rows (decode_down_t1_kernel) up to this batch
+// The down projection by output rows (decode_down_rows_kernel) up to this batch
 // (measured on 48 streamed Qwen3 layers, µs per layer, rows / tiled down:
 // T=1 15.2 / 19.5, T=2 20.1 / 22.6, T=3 24.1 / 23.6, T=4 28.3 / 25.2).
 constexpr int kRowsDownMaxT = 2;
@@ -1247,8 +1247,8 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(LayerArgs a) {
 }
 
 // ---- few tokens: the down projection by output rows ------------------------
-// For a few tokens (T * (k + shared) <= T1_MAX_SLOTS) a work-group owns
-// T1_ROWS output rows across all of the batch's routed slots and sums each
+// For a few tokens (T * (k + shared) <= ROWS_MAX_SLOTS) a work-group owns
+// ROWS_R output rows across all of the batch's routed slots and sums each
 // token's slots itself: no fp32 partial rows, no counters, no combine tail
 // (at T = 1 that tail is most of the down kernel's time).  A slot's weights
 // are read per slot, so an expert routed by several tokens is read again (from
@@ -1263,8 +1263,8 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(LayerArgs a) {
 // lane sums are folded in a fixed order (DPP inside 16-lane rows, then the
 // two rows), and each token's weighted slot rows are summed in ascending slot
 // order: the result does not depend on scheduling.
-constexpr int T1_ROWS = 4;        // output rows per work-group
-constexpr int T1_MAX_SLOTS = 64;  // T * (k + shared)
+constexpr int ROWS_R = 4;        // output rows per work-group
+constexpr int ROWS_MAX_SLOTS = 64;  // T * (k + shared)
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float v) {
@@ -1288,7 +1288,7 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 // its id (no active-expert list is needed).  Lanes take the 32-k chunks
 // c = lane, lane + 32, ... of the token's row of x, permuted into the nibbles'
 // pairing order, and dot2 both rows' dequantised nibbles against it (as in
-// decode_down_t1_kernel); the folded gate and up sums give SiLU(g) * u, stored
+// decode_down_rows_kernel); the folded gate and up sums give SiLU(g) * u, stored
 // in `mid` in INT4 pairing order.
 constexpr int GU_PAIRS = 8;
 
@@ -1366,7 +1366,7 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
     g += f16_bits_to_f32(gs[i]) * (ag - base * xsum);
     u += f16_bits_to_f32(us[i]) * (au - base * xsum);
   }
-  // fold each half-wave's 32 lanes (fixed order), as decode_down_t1_kernel
+  // fold each half-wave's 32 lanes (fixed order), as decode_down_rows_kernel
   auto fold = [&](float v, float& lo, float& hi) {
     v += dpp_f32<0xB1>(v);
     v += dpp_f32<0x4E>(v);
@@ -1394,9 +1394,9 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
 // 16-bit pairs and the row's fp16 scale multiplies the sum).  NCH: 32-k chunks
 // per lane (all of a lane's loads are issued before its arithmetic).
 template <bool BF, bool MIXED, int NCH>
-__global__ void __launch_bounds__(256) decode_down_t1_kernel(LayerArgs a) {
-  constexpr int R = T1_ROWS;
-  __shared__ float red[T1_MAX_SLOTS][R];
+__global__ void __launch_bounds__(256) decode_down_rows_kernel(LayerArgs a) {
+  constexpr int R = ROWS_R;
+  __shared__ float red[ROWS_MAX_SLOTS][R];
   const int h0 = blockIdx.x * R;
   const int lane = threadIdx.x & 63, hw = threadIdx.x >> 5, l = threadIdx.x & 31;
   const int C = a.I >> 5;                  // 32-k chunks per row
@@ -1673,7 +1673,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   // grid is sized for one tile per expert up to T = 16 (more tiles there
   // need repeated ids; the work-groups then stride over the extra units).
   const int64_t max_tiles = d.T <= 16 ? max_active : max_active + ((int64_t)d.T * d.kp + 15) / 16;
-  const bool rows = d.T <= kRowsDownMaxT && d.kp >= 4 && d.T * d.kp <= T1_MAX_SLOTS && d.I <= 2048;
+  const bool rows = d.T <= kRowsDownMaxT && d.kp >= 4 && d.T * d.kp <= ROWS_MAX_SLOTS && d.I <= 2048;
   const bool rows_gu = rows && !mixed && d.T <= kRowsGateUpMaxT && d.I % GU_PAIRS == 0 && d.H <= 4096;
   for (int ph = 0; ph < 2; ++ph) {
     const hipEvent_t* ev = stage_events();
@@ -1694,20 +1694,20 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     }
     if (ph == 1 && rows) {
       // few tokens: the down projection by output rows, summed in-kernel
-      const dim3 g1((unsigned)(d.H / T1_ROWS));
+      const dim3 g1((unsigned)(d.H / ROWS_R));
       const int nch = (d.I / 32 + 31) / 32;  // chunks per lane
       decode_kernel_t k1;
       if (mixed)
-        k1 = nch <= 1 ? (d.bf ? decode_down_t1_kernel<true, true, 1> : decode_down_t1_kernel<false, true, 1>)
-                      : (d.bf ? decode_down_t1_kernel<true, true, 2> : decode_down_t1_kernel<false, true, 2>);
+        k1 = nch <= 1 ? (d.bf ? decode_down_rows_kernel<true, true, 1> : decode_down_rows_kernel<false, true, 1>)
+                      : (d.bf ? decode_down_rows_kernel<true, true, 2> : decode_down_rows_kernel<false, true, 2>);
       else
-        k1 = nch <= 1 ? (d.bf ? decode_down_t1_kernel<true, false, 1> : decode_down_t1_kernel<false, false, 1>)
-                      : (d.bf ? decode_down_t1_kernel<true, false, 2> : decode_down_t1_kernel<false, false, 2>);
+        k1 = nch <= 1 ? (d.bf ? decode_down_rows_kernel<true, false, 1> : decode_down_rows_kernel<false, false, 1>)
+                      : (d.bf ? decode_down_rows_kernel<true, false, 2> : decode_down_rows_kernel<false, false, 2>);
       if (ev)
         hipExtLaunchKernelGGL(k1, g1, dim3(256), 0, s, ev[2], ev[3], 0, a);
       else
         hipLaunchKernelGGL(k1, g1, dim3(256), 0, s, a);
-      return check_launch("decode_down_t1_kernel");
+      return check_launch("decode_down_rows_kernel");
     }
     // per-wave weight slices / partial tiles, then the per-expert row counts
     const size_t lds = (size_t)DW * WAVE_LDS + (((size_t)(d.Ep + 1) / 2 * 4 + 15) & ~(size_t)15);
