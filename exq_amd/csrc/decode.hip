@@ -1188,56 +1188,118 @@ __global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_ke
 // out[t, h..h+3] = sum over the token's slots j (ascending) of weight * the
 // slot's partial row (its k-splits summed in split order first), fp32,
 // rounded once -- the same order and arithmetic as combine_block.  One thread
-// per four consecutive h; the kernel boundary makes every partial row visible.
-template <bool BF>
-__global__ void __launch_bounds__(256) decode_combine_kernel(LayerArgs a) {
+// per four consecutive h, in 64-thread work-groups so that even one token's
+// row spreads over several CUs; the kernel boundary makes every partial row
+// visible.  Slots are taken kCombineBatch at a time: their ids and weights
+// are loaded as raw bits, then the first kCombineBatch (slot, split) partial
+// loads go out, and only then are the ids and weights converted (so the
+// partial loads do not wait behind them: Mixtral's two slots x eight splits
+// at one token are one memory round trip).  A dropped slot's rows were never
+// written: its loads are replaced by zeros.
+constexpr int kCombineThreads = 64;
+constexpr int kCombineBatch = 16;
+
+template <bool BF, bool ID64, int WDT>  // ids int64 / int32; weights EXQ_DTYPE_F32 / _BF16 / _F16
+__global__ void __launch_bounds__(kCombineThreads) decode_combine_kernel(LayerArgs a) {
+  constexpr int CB = kCombineBatch;
+  constexpr bool wf32 = WDT == EXQ_DTYPE_F32;
+  __shared__ float s_w[CB][kCombineThreads];  // this thread's slot weights (0: dropped)
   const int hq = a.H >> 2;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int idx = blockIdx.x * kCombineThreads + threadIdx.x;
   if (idx >= a.T * hq) return;
   const int t = idx / hq;
   const int h = (idx - t * hq) * 4;
   const int64_t set = (int64_t)a.T * a.kp * a.H;  // floats per partial set
   const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, a.nsplit * set * 4);
+  const __amdgpu_buffer_rsrc_t ids_r = make_rsrc(a.ids, (int64_t)a.T * a.k * (ID64 ? 8 : 4));
+  const __amdgpu_buffer_rsrc_t w_r = make_rsrc(a.topk_w, (int64_t)a.T * a.k * (wf32 ? 4 : 2));
+  const float4 zero = float4{0.f, 0.f, 0.f, 0.f};
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  // eight slots at a time: their ids and weights, then every partial load of
-  // the chunk in flight at once (dropped slots load zeros: out-of-range offset)
-  for (int j0 = 0; j0 < a.kp; j0 += 8) {
-    float wg[8];
-    int off[8];
+  for (int j0 = 0; j0 < a.kp; j0 += CB) {
+    const int nsl = a.kp - j0 < CB ? a.kp - j0 : CB;  // slots of this batch
+    // raw ids and weights of slots j0.. (one load each; zeros past the
+    // routed slots)
+    uint32_t lo[CB], hi[CB], wr[CB];
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      const int j = j0 + jj;
-      bool ok = j < a.kp;
-      float wgt = 1.f;
-      if (ok && j < a.k) {
-        const int64_t id = load_index(a.ids, a.ids_dtype, (int64_t)t * a.k + j);
-        wgt = load_as_f32(a.topk_w, a.w_dtype, (int64_t)t * a.k + j);
-        ok = id >= 0 && id < a.E;
+    for (int i = 0; i < CB; ++i) {
+      const int q = t * a.k + j0 + i;
+      const bool in = i < nsl && j0 + i < a.k;
+      if constexpr (ID64) {
+        const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(ids_r, in ? q * 8 : OOB_OFF, 0, 0);
+        lo[i] = v[0];
+        hi[i] = v[1];
+      } else {
+        lo[i] = __builtin_amdgcn_raw_buffer_load_b32(ids_r, in ? q * 4 : OOB_OFF, 0, 0);
+        hi[i] = 0u;
       }
-      wg[jj] = ok ? wgt : 0.f;
-      off[jj] = ok ? ((t * a.kp + j) * a.H + h) * 4 : OOB_OFF;
+      if constexpr (wf32)
+        wr[i] = __builtin_amdgcn_raw_buffer_load_b32(w_r, in ? q * 4 : OOB_OFF, 0, 0);
+      else
+        wr[i] = __builtin_amdgcn_raw_buffer_load_b16(w_r, in ? q * 2 : OOB_OFF, 0, 0);
     }
-    float4 pv[8];
+    const int n_it = nsl * a.nsplit;  // item q: slot j0 + q / nsplit, split q % nsplit
+    uint32_t okm = 0u;                // bit i: slot j0 + i is routed
+    int jj = 0, sp = 0;               // slot (from j0) and split of the next item
+    float4 cur = zero;                // the current slot's splits so far
+    float cw = 0.f;
+    float4 pv[CB];
+    // items q0.. of the batch: every partial load in flight at once
+    auto issue = [&](int q0) {
+      int js = jj, ss = sp;
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-      pv[jj] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(part_r, off[jj], 0, 0));
-    for (int sp = 1; sp < a.nsplit; ++sp) {  // further k-splits, in split order
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const float4 q = __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(
-                        part_r, off[jj] == OOB_OFF ? OOB_OFF : (int)(off[jj] + sp * set * 4), 0, 0));
-        pv[jj].x += q.x; pv[jj].y += q.y; pv[jj].z += q.z; pv[jj].w += q.w;
+      for (int i = 0; i < CB; ++i) {
+        const int off = q0 + i < n_it
+                            ? (int)((ss * set + (int64_t)(t * a.kp + j0 + js) * a.H + h) * 4)
+                            : OOB_OFF;
+        pv[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(part_r, off, 0, 0));
+        if (++ss == a.nsplit) {
+          ss = 0;
+          ++js;
+        }
       }
+    };
+    auto accumulate = [&](int q0) {
+#pragma unroll
+      for (int i = 0; i < CB; ++i) {
+        if (q0 + i < n_it) {
+          if (sp == 0) {
+            const bool ok = (okm >> jj) & 1u;
+            cw = s_w[jj][threadIdx.x];
+            cur = ok ? pv[i] : zero;
+          } else if ((okm >> jj) & 1u) {  // further k-splits, in split order
+            cur.x += pv[i].x; cur.y += pv[i].y; cur.z += pv[i].z; cur.w += pv[i].w;
+          }
+          if (sp == a.nsplit - 1) {
+            acc[0] += cw * cur.x;
+            acc[1] += cw * cur.y;
+            acc[2] += cw * cur.z;
+            acc[3] += cw * cur.w;
+          }
+          if (++sp == a.nsplit) {
+            sp = 0;
+            ++jj;
+          }
+        }
+      }
+    };
+    issue(0);
+    // the slots' ids and weights, converted after the partial loads are out
+#pragma unroll
+    for (int i = 0; i < CB; ++i) {
+      const int j = j0 + i;
+      const int64_t id = ID64 ? (int64_t)(((uint64_t)hi[i] << 32) | lo[i]) : (int64_t)(int32_t)lo[i];
+      const bool ok = j >= a.k || (id >= 0 && id < a.E);  // shared experts: weight 1
+      const float wf = j >= a.k                  ? 1.f
+                       : wf32                    ? __builtin_bit_cast(float, wr[i])
+                       : WDT == EXQ_DTYPE_BF16 ? bf16_bits_to_f32(wr[i])
+                                                 : f16_bits_to_f32(wr[i]);
+      okm |= (ok ? 1u : 0u) << i;
+      s_w[i][threadIdx.x] = ok ? wf : 0.f;
     }
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      if (j0 + jj < a.kp) {
-        acc[0] += wg[jj] * pv[jj].x;
-        acc[1] += wg[jj] * pv[jj].y;
-        acc[2] += wg[jj] * pv[jj].z;
-        acc[3] += wg[jj] * pv[jj].w;
-      }
+    accumulate(0);
+    for (int q0 = CB; q0 < n_it; q0 += CB) {
+      issue(q0);
+      accumulate(q0);
     }
   }
   uint2 o;
@@ -1590,6 +1652,17 @@ decode_kernel_t pick_ph(bool mixed, int path) {
 // re-reads its weight slice, from L2), which measured faster at T = 32 and 64
 // than kernels holding two or four tiles per pass (higher register use, lower
 // occupancy).
+template <bool BF, bool ID64>
+decode_kernel_t pick_combine_w(int w_dtype) {
+  return w_dtype == EXQ_DTYPE_F32    ? decode_combine_kernel<BF, ID64, EXQ_DTYPE_F32>
+         : w_dtype == EXQ_DTYPE_BF16 ? decode_combine_kernel<BF, ID64, EXQ_DTYPE_BF16>
+                                     : decode_combine_kernel<BF, ID64, EXQ_DTYPE_F16>;
+}
+decode_kernel_t pick_combine(bool bf, bool id64, int w_dtype) {
+  if (bf) return id64 ? pick_combine_w<true, true>(w_dtype) : pick_combine_w<true, false>(w_dtype);
+  return id64 ? pick_combine_w<false, true>(w_dtype) : pick_combine_w<false, false>(w_dtype);
+}
+
 decode_kernel_t pick_kernel(bool bf, int ph, bool mixed, int path) {
   if (bf) return ph == 0 ? pick_ph<true, 0>(mixed, path) : pick_ph<true, 1>(mixed, path);
   return ph == 0 ? pick_ph<false, 0>(mixed, path) : pick_ph<false, 1>(mixed, path);
@@ -1771,12 +1844,12 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     int st = check_launch(ph == 0 ? "moe_decode_kernel<gate/up>" : "moe_decode_kernel<down>");
     if (st) return st;
     if (tail) {
-      const dim3 cg((unsigned)cdiv((int64_t)d.T * (d.H / 4), 256));
-      const auto ck = d.bf ? decode_combine_kernel<true> : decode_combine_kernel<false>;
+      const dim3 cg((unsigned)cdiv((int64_t)d.T * (d.H / 4), kCombineThreads));
+      const decode_kernel_t ck = pick_combine(d.bf, d.ids_dtype == EXQ_DTYPE_I64, d.w_dtype);
       if (ev)
-        hipExtLaunchKernelGGL(ck, cg, dim3(256), 0, s, nullptr, ev[3], 0, a);
+        hipExtLaunchKernelGGL(ck, cg, dim3(kCombineThreads), 0, s, nullptr, ev[3], 0, a);
       else
-        hipLaunchKernelGGL(ck, cg, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(ck, cg, dim3(kCombineThreads), 0, s, a);
       st = check_launch("decode_combine_kernel");
       if (st) return st;
     }

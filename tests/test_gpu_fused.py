@@ -132,21 +132,28 @@ def test_workspace_contents_do_not_matter(device):
     values that would trigger an early combine) give the same bits."""
     from exq_amd.kernels import fused_experts
     from exq_amd.kernels.fused_moe import moe_workspace_bytes
-    cfg = synth.CONFIGS["qwen3"]
-    p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, synth.seed_for(cfg), device)
     gen = torch.Generator(device="cpu").manual_seed(3)
-    for T in (1, 16, 64):
-        banner(f"dirty workspace qwen3 T={T}")
-        ids, w, tid, tw = _routing(cfg, T, device)
-        x = _hidden(T, cfg.hidden, 2, device)
-        nbytes = moe_workspace_bytes(T, cfg.hidden, cfg.inter, cfg.n_experts, cfg.top_k)
-        clean = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        want = fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=clean)
-        ones = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=device)
-        rnd = torch.randint(0, 256, (nbytes,), generator=gen, dtype=torch.uint8).to(device)
-        for ws in (ones, rnd):
-            assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws), want)
-            assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws), want)
+    # Qwen3 at 1 / 16 / 64 tokens, and a top-2 layer at one token (the gate/up
+    # kernel by output rows before the tiled down kernel's in-kernel combine)
+    top2 = synth.MoeConfig("top2", 34, 1024, 512, 8, 2, True, zipf=False)
+    for cfg, Ts in ((synth.CONFIGS["qwen3"], (1, 16, 64)), (top2, (1,))):
+        p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, synth.seed_for(cfg),
+                                     device)
+        for T in Ts:
+            banner(f"dirty workspace {cfg.name} T={T}")
+            ids, w, tid, tw = _routing(cfg, T, device)
+            x = _hidden(T, cfg.hidden, 2, device)
+            nbytes = moe_workspace_bytes(T, cfg.hidden, cfg.inter, cfg.n_experts, cfg.top_k)
+            clean = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            want = fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=clean)
+            if cfg is top2:
+                assert_close_rel(want, oracle_int4_layer(x, p13, s13, p2, s2, ids, w), TOL,
+                                 f"top-2 T={T}")
+            ones = torch.full((nbytes,), 0xFF, dtype=torch.uint8, device=device)
+            rnd = torch.randint(0, 256, (nbytes,), generator=gen, dtype=torch.uint8).to(device)
+            for ws in (ones, rnd):
+                assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws), want)
+                assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws), want)
 
 
 def test_fused_dropped_ids_and_edges(device):
