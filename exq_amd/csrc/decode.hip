@@ -68,6 +68,7 @@ constexpr int MAX_SLOTS = 1024;    // T * (k + n_shared)
 constexpr int MAX_BM_WORDS = 32;   // active-expert bitmap: E + shared <= 1024
 constexpr int kCombineLaunchMinT = 32;     // down combine: own launch from this batch on,
 constexpr int kCombineLaunchMinSplit = 4;  // or from this many k-splits on; else in-kernel
+static_assert(kCombineLaunchMinSplit <= 4, "the in-kernel combine sums at most three k-splits");
 // The down projection by output rows (decode_down_rows_kernel) up to this batch
 // (measured on 48 streamed Qwen3 layers, µs per layer, rows / tiled down:
 // T=1 15.2 / 19.5, T=2 20.1 / 22.6, T=3 24.1 / 23.6, T=4 28.3 / 25.2).
@@ -449,52 +450,72 @@ __device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TI
 }
 
 // Down phase: the last of a column block's units (by its counter) combines
-// the block.
-template <bool BF, int ROWS_B>
-__device__ __forceinline__ void combine_block(const LayerArgs& a, const Route& rt, int blk) {
-  // out[t, h..h+3] = sum over the token's slots j (ascending) of weight *
-  // partial; a chunk of eight slots' loads is issued at once
+// the block: out[t, h..h+3] = sum over the token's slots j (ascending) of
+// weight * partial (the NS k-splits of a slot summed in split order first).
+// Slots are taken 8 / NS at a time: all of a batch's partial loads and the
+// raw router weights of its slots go out before any of them is used, so
+// a batch is one memory round trip (NS and the weight width are template
+// arguments, so every load lands in a register of its own with no branch
+// between the loads and their use).
+template <bool BF, int ROWS_B, int NS, bool WF32>  // WF32: fp32 router weights (else 16-bit)
+__device__ __forceinline__ void combine_block_ns(const LayerArgs& a, const Route& rt, int blk) {
+  constexpr int SB = 8 / NS;  // slots per batch (eight slots: every k + shared of these configurations)
+  constexpr bool wf32 = WF32;
   const int64_t set = (int64_t)a.T * a.kp * a.H;  // floats per partial set
   const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, a.nsplit * set * 4);
+  const __amdgpu_buffer_rsrc_t w_r = make_rsrc(a.topk_w, (int64_t)a.T * a.k * (wf32 ? 4 : 2));
   const int h0 = blk * ROWS_B;
   for (int idx = threadIdx.x; idx < a.T * (ROWS_B / 4); idx += DNT) {
     const int t = idx / (ROWS_B / 4);
     const int h = h0 + (idx - t * (ROWS_B / 4)) * 4;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < a.kp; j0 += 8) {
-      float4 pv[8];
-      float wg[8];
+    for (int j0 = 0; j0 < a.kp; j0 += SB) {
+      float4 pv[SB][NS];
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int j = j0 + jj;
-        bool ok = j < a.kp;
-        float wgt = 1.f;
-        if (ok && j < a.k) {
-          ok = rt.ids[t * a.k + j] >= 0;
-          if (ok) wgt = load_as_f32(a.topk_w, a.w_dtype, (int64_t)t * a.k + j);
-        }
-        wg[jj] = ok ? wgt : 0.f;
-        pv[jj] = __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(
-                        part_r, ok ? ((t * a.kp + j) * a.H + h) * 4 : OOB_OFF, 0,
-                        CPOL_SC1));
-        // further k-splits of the same row, in split order
-        for (int sp = 1; sp < a.nsplit; ++sp) {
-          const float4 q = __builtin_bit_cast(
+      for (int i = 0; i < SB; ++i)
+#pragma unroll
+        for (int sp = 0; sp < NS; ++sp)
+          pv[i][sp] = __builtin_bit_cast(
               float4, __builtin_amdgcn_raw_buffer_load_b128(
                           part_r,
-                          ok ? (int)((sp * set + (int64_t)(t * a.kp + j) * a.H + h) * 4) : OOB_OFF, 0,
-                          CPOL_SC1));
-          pv[jj].x += q.x; pv[jj].y += q.y; pv[jj].z += q.z; pv[jj].w += q.w;
-        }
+                          j0 + i < a.kp ? (int)((sp * set + (int64_t)(t * a.kp + j0 + i) * a.H + h) * 4)
+                                        : OOB_OFF,
+                          0, CPOL_SC1));
+      // (the weights after the partial loads: converting them waits for
+      // loads that are all in flight already)
+      // raw weights of the routed slots (zeros otherwise)
+      uint32_t wr[SB];
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const int q = t * a.k + j0 + i;
+        const bool in = j0 + i < a.k;
+        if constexpr (WF32)
+          wr[i] = __builtin_amdgcn_raw_buffer_load_b32(w_r, in ? q * 4 : OOB_OFF, 0, 0);
+        else
+          wr[i] = __builtin_amdgcn_raw_buffer_load_b16(w_r, in ? q * 2 : OOB_OFF, 0, 0);
       }
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        if (j0 + jj < a.kp) {
-          acc[0] += wg[jj] * pv[jj].x;
-          acc[1] += wg[jj] * pv[jj].y;
-          acc[2] += wg[jj] * pv[jj].z;
-          acc[3] += wg[jj] * pv[jj].w;
+      for (int i = 0; i < SB; ++i) {
+        const int j = j0 + i;
+        if (j < a.kp) {
+          // a dropped slot's partial rows were never written: zeros instead
+          const bool ok = j >= a.k || rt.ids[t * a.k + j] >= 0;
+          const float wf = j >= a.k                    ? 1.f
+                           : wf32                      ? __builtin_bit_cast(float, wr[i])
+                           : a.w_dtype == EXQ_DTYPE_BF16 ? bf16_bits_to_f32(wr[i])
+                                                         : f16_bits_to_f32(wr[i]);
+          const float wg = ok ? wf : 0.f;
+          const float4 zero = float4{0.f, 0.f, 0.f, 0.f};
+          float4 cur = ok ? pv[i][0] : zero;
+#pragma unroll
+          for (int sp = 1; sp < NS; ++sp) {  // further k-splits, in split order
+            const float4 q = ok ? pv[i][sp] : zero;
+            cur.x += q.x; cur.y += q.y; cur.z += q.z; cur.w += q.w;
+          }
+          acc[0] += wg * cur.x;
+          acc[1] += wg * cur.y;
+          acc[2] += wg * cur.z;
+          acc[3] += wg * cur.w;
         }
       }
     }
@@ -503,6 +524,18 @@ __device__ __forceinline__ void combine_block(const LayerArgs& a, const Route& r
     o.y = to_act_bits<BF>(acc[2]) | (to_act_bits<BF>(acc[3]) << 16);
     *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.H + h) = o;
   }
+}
+
+template <bool BF, int ROWS_B>
+__device__ __forceinline__ void combine_block(const LayerArgs& a, const Route& rt, int blk) {
+  // in-kernel combines run with fewer than kCombineLaunchMinSplit splits
+  const bool wf32 = a.w_dtype == EXQ_DTYPE_F32;
+  if (a.nsplit == 1)
+    wf32 ? combine_block_ns<BF, ROWS_B, 1, true>(a, rt, blk) : combine_block_ns<BF, ROWS_B, 1, false>(a, rt, blk);
+  else if (a.nsplit == 2)
+    wf32 ? combine_block_ns<BF, ROWS_B, 2, true>(a, rt, blk) : combine_block_ns<BF, ROWS_B, 2, false>(a, rt, blk);
+  else
+    wf32 ? combine_block_ns<BF, ROWS_B, 3, true>(a, rt, blk) : combine_block_ns<BF, ROWS_B, 3, false>(a, rt, blk);
   __syncthreads();
   if (threadIdx.x == 0) {
     __hip_atomic_store(sync_c(a, blk), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
