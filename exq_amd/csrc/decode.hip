@@ -152,18 +152,35 @@ __device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t* cnt
   const int lane = threadIdx.x & 63;
   const int n = a.T * a.k;
   const int nw = (a.Ep + 31) >> 5;
+  // this thread's ids (s = threadIdx.x + i * DNT), loaded as raw words before
+  // the LDS clear and its barrier, all in flight at once (no dtype branch or
+  // conversion between the loads)
+  constexpr int RPT = MAX_SLOTS / DNT;
+  const bool id64 = a.ids_dtype == EXQ_DTYPE_I64;
+  const __amdgpu_buffer_rsrc_t ids_r = make_rsrc(a.ids, (int64_t)n * (id64 ? 8 : 4));
+  uint32_t lo[RPT], hi[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int s = threadIdx.x + i * DNT;
+    lo[i] = __builtin_amdgcn_raw_buffer_load_b32(ids_r, s < n ? s * (id64 ? 8 : 4) : OOB_OFF, 0, 0);
+    hi[i] = __builtin_amdgcn_raw_buffer_load_b32(ids_r, s < n && id64 ? s * 8 + 4 : OOB_OFF, 0, 0);
+  }
   if (threadIdx.x < MAX_BM_WORDS) r.bitmap[threadIdx.x] = 0u;
   if (threadIdx.x == 0) r.multi = a.T > 16 && a.Ep > a.E;  // shared experts take every token
   for (int i = threadIdx.x; i < (a.Ep + 1) >> 1; i += DNT) cntw[i] = 0u;
   __syncthreads();
-  for (int s = threadIdx.x; s < n; s += DNT) {
-    const int64_t id = load_index(a.ids, a.ids_dtype, s);
-    const int v = (id >= 0 && id < a.E) ? (int)id : -1;
-    r.ids[s] = (int16_t)v;
-    if (v >= 0) {
-      atomicOr(&r.bitmap[v >> 5], 1u << (v & 31));
-      const uint32_t old = atomicAdd(&cntw[v >> 1], 1u << ((v & 1) * 16));
-      if (((old >> ((v & 1) * 16)) & 0xffffu) >= 16u) r.multi = 1;
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int s = threadIdx.x + i * DNT;
+    if (s < n) {
+      const int64_t id = id64 ? (int64_t)(((uint64_t)hi[i] << 32) | lo[i]) : (int64_t)(int32_t)lo[i];
+      const int v = (id >= 0 && id < a.E) ? (int)id : -1;
+      r.ids[s] = (int16_t)v;
+      if (v >= 0) {
+        atomicOr(&r.bitmap[v >> 5], 1u << (v & 31));
+        const uint32_t old = atomicAdd(&cntw[v >> 1], 1u << ((v & 1) * 16));
+        if (((old >> ((v & 1) * 16)) & 0xffffu) >= 16u) r.multi = 1;
+      }
     }
   }
   if (threadIdx.x < a.Ep - a.E && a.T > 0) {
