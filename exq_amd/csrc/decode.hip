@@ -47,6 +47,8 @@
 // first on the same stream, zeroes the down kernel's counters, so the
 // workspace needs no zero fill and an interrupted call leaves nothing behind
 // for the next one; the last combine zeroes them again as well.
+#include <type_traits>
+
 #include "exq_internal.h"
 
 #include <hip/hip_ext.h>
@@ -974,7 +976,12 @@ template <int TIER, bool BF, int PH, int NT>
 __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& rt, int e, int blk,
                                               int sp, int tile, unsigned char* lds) {
   using G = Geo<TIER, PH, NT>;
-  constexpr int RS = G::RS, QPK = G::QPK, P = G::P, WSLOT = G::WSLOT;
+  constexpr int RS = G::RS, QPK = G::QPK, P = G::P;
+  // BF16 and INT8 down units take their 64 rows in two passes of 32, so that
+  // a ring slot holds half the weight registers (32 instead of 64 for BF16)
+  constexpr int RSP = (TIER != 2 && PH == 1) ? RS / 2 : RS;  // row sets per pass
+  constexpr int NPASS = RS / RSP;
+  using pass0_t = std::integral_constant<int, 0>;
   const UnitCtx<TIER, PH, NT> u(a, e, blk, sp);
   int voff[RS];
 #pragma unroll
@@ -1012,19 +1019,20 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
         sc_lds[((rs * 16 + u.r16) * nd * 4 + e0) / 2 + ((kb >> a.gshift) - g_lo)]);
   };
 
-  uint4 wreg[P][WSLOT];
+  uint4 wreg[P][RSP * QPK];
   uint4 areg[P][4 * NT];
   int xo[NT];
-  auto load_w = [&](int p, int kbl) {
+  auto load_w = [&](int p, int kbl, auto rs0c) {  // row sets rs0 .. rs0 + RSP - 1
+    constexpr int rs0 = decltype(rs0c)::value;
     const bool ok = uni_b(kbl < u.nmy);
     const __amdgpu_buffer_rsrc_t r = ok ? u.wr : u.wnull;
     const int kb = uni_i(ok ? u.lo + kbl : u.lo);
 #pragma unroll
-    for (int rs = 0; rs < RS; ++rs) {
+    for (int rs = 0; rs < RSP; ++rs) {
 #pragma unroll
       for (int h = 0; h < QPK; ++h)
         wreg[p][rs * QPK + h] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff[rs] + h * 16, kb * G::KBSTRIDE, 0));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff[rs0 + rs] + h * 16, kb * G::KBSTRIDE, 0));
     }
   };
   auto load_a = [&](int p, int kbl) {
@@ -1040,7 +1048,7 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
   };
 
 #pragma unroll
-  for (int p = 0; p < P; ++p) load_w(p, p);
+  for (int p = 0; p < P; ++p) load_w(p, p, pass0_t{});
   // this unit's rows: tile `tile` of the expert's rows (one pass)
   const int r_begin = tile * NT * 16;
   int sl[NT];
@@ -1064,6 +1072,9 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
       if (r0 == 0) wait_vm_le<P * (RS * QPK + 4 * NT)>();
     }
 
+    // the k-loop over row sets rs0 .. rs0 + RSP - 1 (ring already filled)
+    auto kloop = [&](auto rs0c) {
+    constexpr int rs0 = decltype(rs0c)::value;
     for (int kb0 = 0; kb0 < u.nmy; kb0 += P) {
 #pragma unroll
       for (int p = 0; p < P; ++p) {
@@ -1077,7 +1088,7 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
             bfr[2] = ddeq4(w.z, dq_mask, dq_magic);
             bfr[3] = ddeq4(w.w, dq_mask, dq_magic);
             // past the wave's range the activations (so acc) are zero
-            sc = kb0 + p < u.nmy ? scale_at(rs, u.lo + kb0 + p) : 0.f;
+            sc = kb0 + p < u.nmy ? scale_at(rs0 + rs, u.lo + kb0 + p) : 0.f;
           } else if constexpr (TIER == 1) {
             const uint4 w0 = wreg[p][rs * QPK + 0], w1 = wreg[p][rs * QPK + 1];
             const uint2 d0 = ddeq8<BF>(w0.x), d1 = ddeq8<BF>(w0.y);
@@ -1099,14 +1110,14 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
           f32x4_t init;
           make_a<TIER, BF, PH>(&areg[p][0], xa, init);
 #pragma unroll
-          for (int rs = 0; rs < RS; ++rs) {
+          for (int rs = 0; rs < RSP; ++rs) {
             uint4 bfr[4];
             float sc;
             dequant(rs, bfr, sc);
             f32x4_t acc = init;
 #pragma unroll
             for (int d = 0; d < 4; ++d) acc = dmfma<BF>(xa[d], bfr[d], acc);
-            tot[rs][0] += sc * acc;
+            tot[rs0 + rs][0] += sc * acc;
           }
         } else {
           // several tiles: one tile's A operand at a time (fewer live registers)
@@ -1117,23 +1128,33 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
               f32x4_t init;
               make_a<TIER, BF, PH>(&areg[p][tt * 4], xa, init);
 #pragma unroll
-              for (int rs = 0; rs < RS; ++rs) {
+              for (int rs = 0; rs < RSP; ++rs) {
                 uint4 bfr[4];
                 float sc;
                 dequant(rs, bfr, sc);
                 f32x4_t acc = init;
 #pragma unroll
                 for (int d = 0; d < 4; ++d) acc = dmfma<BF>(xa[d], bfr[d], acc);
-                tot[rs][tt] += sc * acc;
+                tot[rs0 + rs][tt] += sc * acc;
               }
             }
           }
         }
-        load_w(p, kb0 + p + P);  // refill this ring slot (zeros past the range)
+        load_w(p, kb0 + p + P, rs0c);  // refill this ring slot (zeros past the range)
         load_a(p, kb0 + p + P);
         // keep the ring order: slot p's refill is issued before slot p+1 is consumed
         __builtin_amdgcn_sched_barrier(0);
       }
+    }
+    };
+    kloop(pass0_t{});
+    if constexpr (NPASS == 2) {  // the second half of the rows: fill the ring again
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        load_w(p, p, std::integral_constant<int, RSP>{});
+        load_a(p, p);
+      }
+      kloop(std::integral_constant<int, RSP>{});
     }
     float4* red = reinterpret_cast<float4*>(lds + u.wave * WAVE_LDS);
 #pragma unroll
@@ -1152,10 +1173,14 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
 // A grid of at most one resident round of work-groups; each routes once and
 // then takes units blockIdx.x, blockIdx.x + gridDim.x, ... (expert-major:
 // unit u is row block u % nb of the (u / nb)-th active expert).
-// Four waves per SIMD (four work-groups per CU, at most 128 VGPRs) except
-// the mixed-tier down kernel, whose register use needs two.
+// Four waves per SIMD (four work-groups per CU, at most 128 VGPRs), the
+// mixed-tier down kernel included: its BF16 and INT8 units hold their 64
+// weight rows in two passes of 32 (run_unit_ring), which keeps it within 128
+// registers without spills (at two waves per SIMD it left half the resident
+// slots empty: DeepSeek-V2-Lite T=64 120.5 -> 118.0 us, the mixed OLMoE
+// stack at T=32 88.9 -> 87.0).
 template <bool BF, int PH, int NT, bool MIXED, int PATH>  // INT4 path: 0 ring, 1 LDS, 2 chunked LDS
-__global__ void __launch_bounds__(DNT, (PH == 1 && MIXED) ? 2 : 4) moe_decode_kernel(LayerArgs a) {
+__global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
   __shared__ Route rt;
   __shared__ int s_flag;
