@@ -67,3 +67,57 @@ def test_combine_paths_dtypes_and_dropped_ids(I, T, device):
     assert torch.count_nonzero(out[0]) == 0
     ref = oracle_int4_layer(x, p13, s13, p2, s2, allbad, w)
     assert_close_rel(out, ref, TOL, f"combine I={I} T={T} token 0 dropped")
+
+
+@pytest.mark.parametrize("I,T,E,k", [(512, 3, 16, 12), (512, 40, 32, 20)])
+def test_combine_more_slots_than_one_batch(I, T, E, k, device):
+    """More slots per token than one load batch holds.  The in-kernel combine
+    takes eight slots per batch, so top-12 at three tokens takes two batches.
+    The combine launch takes 16 (slot, split) items per batch, so top-20 at
+    40 tokens takes two."""
+    from exq_amd.kernels import fused_experts, pack_experts_int4
+    cfg = synth.MoeConfig(f"combine_k{k}", 36, H, I, E, k, True, zipf=False)
+    banner(f"combine top-{k} T={T}")
+    w13, w2 = synth.expert_weights_gpu(E, I, H, 900 + k, device)
+    p13, s13 = pack_experts_int4(w13)
+    p2, s2 = pack_experts_int4(w2)
+    del w13, w2
+    ids, w = synth.routing(cfg, T, 0)
+    ids = ids.copy()
+    ids[0, k - 1] = -1  # dropped, in the second batch
+    ids[1, 3] = -1
+    x = torch.from_numpy(synth.hidden_np(T, H, 6 + T)).to(torch.bfloat16).to(device)
+    for wd in (torch.float32, torch.bfloat16):
+        tw = torch.from_numpy(w).to(wd).to(device)
+        tid = torch.from_numpy(ids).to(device)
+        out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+        ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, tw.float().cpu().numpy())
+        assert_close_rel(out, ref, TOL, f"combine top-{k} T={T} w={wd}")
+        assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid), out)
+
+
+@pytest.mark.parametrize("I,T", [(512, 3), (1536, 3), (1024, 40)])
+def test_combine_shared_experts(I, T, device):
+    """Shared experts (every token, weight 1, slots k .. k + S - 1) through
+    both combines.  The bank has 8 INT4 routed experts, top-2 routing and two
+    INT4 shared experts: one and three k-splits in-kernel at three tokens, and
+    the combine launch at 40 tokens."""
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    from tests.test_gpu_mixed import _oracle
+    E, S, k = 8, 2, 2
+    cfg = synth.MoeConfig(f"combine_shared_{I}", 37, H, I, E, k, True, zipf=False)
+    banner(f"combine shared I={I} T={T}")
+    w13, w2 = synth.expert_weights_gpu(E, I, H, 950 + I, device)
+    s13, s2 = synth.expert_weights_gpu(S, I, H, 960 + I, device)
+    bank = MixedExpertBank.from_weights(w13, w2, [2] * E, shared_w13=s13, shared_w2=s2,
+                                        shared_tier=2)
+    del w13, w2, s13, s2
+    ids, w = synth.routing(cfg, T, 0)
+    ids = ids.copy()
+    ids[0, 0] = -1  # a dropped routed slot: the shared slots still count
+    x = torch.from_numpy(synth.hidden_np(T, H, 8 + T)).to(torch.bfloat16).to(device)
+    tid = torch.from_numpy(ids).to(device)
+    tw = torch.from_numpy(w).to(device)
+    out = fused_experts_mixed(x, bank, tw, tid)
+    assert_close_rel(out, _oracle(bank, x, ids, w), TOL, f"combine shared I={I} T={T}")
+    assert torch.equal(fused_experts_mixed(x, bank, tw, tid), out)
