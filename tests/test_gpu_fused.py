@@ -237,6 +237,27 @@ def test_fused_chunked_gateup(H, I, gs, T, device):
     assert_close_rel(out, ref, TOL, f"chunked H={H} gs={gs} T={T}")
 
 
+@pytest.mark.parametrize("T", [33, 64])
+def test_fused_chunked_gateup_multi_tile(T, device):
+    """Hidden size 4096 (chunked gate/up) with two experts that every token
+    routes to: each expert has T rows, so its later 16-row tiles are units of
+    their own in the later tile segments of both kernels."""
+    from exq_amd.kernels import fused_experts, pack_experts_int4
+    H, I = 4096, 256
+    cfg = synth.MoeConfig("chunk_multi", 38, H, I, 2, 2, True, zipf=False)
+    banner(f"fused chunked multi-tile T={T}")
+    w13, w2 = synth.expert_weights_gpu(2, I, H, 720 + T, device)
+    p13, s13 = pack_experts_int4(w13)
+    p2, s2 = pack_experts_int4(w2)
+    ids, w, tid, tw = _routing(cfg, T, device)
+    assert (np.sort(ids, axis=1) == np.array([0, 1])).all()
+    x = _hidden(T, H, 10 + T, device)
+    out = fused_experts(x, p13, s13, p2, s2, tw, tid)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, f"chunked multi-tile T={T}")
+    assert torch.equal(fused_experts(x, p13, s13, p2, s2, tw, tid), out)
+
+
 def test_moe_int4_forward_sorted_output(device):
     from exq_amd.kernels import moe_int4_forward, sort_tokens_by_expert
     from oracle import moe
