@@ -271,7 +271,8 @@ size_t exq_moe_workspace_size(const exq_moe_problem* problem);
  * SiLU-and-mul, down INT4 GEMM, top-k weighted combine.  Decode batches
  * (T <= 64) run as two kernels (gate/up + SiLU, down + combine) that route
  * for themselves (for one or two tokens the down kernel owns output rows
- * across all routed slots and sums them itself; from 32 tokens a third launch
+ * across all routed slots and sums them itself; from 32 tokens, or when large
+ * experts split each down contraction four or more ways, a third launch
  * combines); larger batches as routing plan + two grouped MFMA GEMMs +
  * combine.  H, I multiples of 32 and a group size that is a multiple of 32
  * dividing both; shapes whose H, I or group size is not a multiple of 128
