@@ -149,8 +149,11 @@ struct Route {
 // select_expert.
 // Also counts each expert's rows into cntw (16 bits per expert, two per word;
 // a count is at most T * k <= MAX_SLOTS, so no carry crosses a half).
+// MAP (mixed banks): also writes emap[e] = (tier << 16) | row of expert e in
+// its tier's bank, for every expert, from loads issued beside the id loads.
+template <bool MAP = false>
 __device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t* cntw, uint32_t& word,
-                                     int& incl, int& c) {
+                                     int& incl, int& c, int* emap = nullptr) {
   const int lane = threadIdx.x & 63;
   const int n = a.T * a.k;
   const int nw = (a.Ep + 31) >> 5;
@@ -167,10 +170,29 @@ __device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t* cnt
     lo[i] = __builtin_amdgcn_raw_buffer_load_b32(ids_r, s < n ? s * (id64 ? 8 : 4) : OOB_OFF, 0, 0);
     hi[i] = __builtin_amdgcn_raw_buffer_load_b32(ids_r, s < n && id64 ? s * 8 + 4 : OOB_OFF, 0, 0);
   }
+  constexpr int EPT = MAP ? kDecodeMaxBuckets / DNT : 1;  // experts per thread
+  uint32_t mt[EPT], mi[EPT];
+  if constexpr (MAP) {
+    const __amdgpu_buffer_rsrc_t tier_r = make_rsrc(a.tier, a.Ep);
+    const __amdgpu_buffer_rsrc_t idx_r = make_rsrc(a.index, a.index ? (int64_t)a.Ep * 4 : 0);
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = threadIdx.x + i * DNT;
+      mt[i] = __builtin_amdgcn_raw_buffer_load_b8(tier_r, e < a.Ep ? e : OOB_OFF, 0, 0);
+      mi[i] = __builtin_amdgcn_raw_buffer_load_b32(idx_r, e < a.Ep ? e * 4 : OOB_OFF, 0, 0);
+    }
+  }
   if (threadIdx.x < MAX_BM_WORDS) r.bitmap[threadIdx.x] = 0u;
   if (threadIdx.x == 0) r.multi = a.T > 16 && a.Ep > a.E;  // shared experts take every token
   for (int i = threadIdx.x; i < (a.Ep + 1) >> 1; i += DNT) cntw[i] = 0u;
   __syncthreads();
+  if constexpr (MAP) {
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+      const int e = threadIdx.x + i * DNT;
+      if (e < a.Ep) emap[e] = (int)((mt[i] << 16) | (a.index ? mi[i] : (uint32_t)e));
+    }
+  }
 #pragma unroll
   for (int i = 0; i < RPT; ++i) {
     const int s = threadIdx.x + i * DNT;
@@ -325,7 +347,8 @@ struct UnitCtx {
   float rowscale[G::RS];
 
   int split;  // down: this unit's k-split (its partial set)
-  __device__ __forceinline__ UnitCtx(const LayerArgs& a, int e, int blk, int sp = 0) {
+  __device__ __forceinline__ UnitCtx(const LayerArgs& a, int e, int blk, int sp = 0,
+                                     int widx_in = -1) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     r16 = lane & 15;
@@ -340,7 +363,8 @@ struct UnitCtx {
     nmy = s0 + (((wave + 1) * (s1 - s0)) >> 2) - lo;  // k-blocks of this wave
     const Proj& W = PH == 0 ? a.w13 : a.w2;
     const int n_rows = PH == 0 ? 2 * a.I : a.H;
-    const int widx = a.index ? uni_i(a.index[uni_i(e)]) : e;
+    // the expert's row in its tier's bank (from the LDS map when the caller has it)
+    const int widx = widx_in >= 0 ? widx_in : (a.index ? uni_i(a.index[uni_i(e)]) : e);
     ebase = (int64_t)widx * n_rows;
     rowbytes = TIER == 2 ? K / 2 : (TIER == 1 ? K : 2 * K);
     const unsigned char* wbase =
@@ -590,11 +614,11 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
 // register ring.
 template <bool BF, int PH, int NT>
 __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt, int e, int blk,
-                                             int sp, int tile, unsigned char* lds) {
+                                             int sp, int tile, unsigned char* lds, int widx = -1) {
   using G = Geo<2, PH, NT>;
   constexpr int RS = G::RS, CK = G::CK;
   constexpr int DA = NT == 4 ? 1 : 2;  // activation k-blocks in flight
-  const UnitCtx<2, PH, NT> u(a, e, blk, sp);
+  const UnitCtx<2, PH, NT> u(a, e, blk, sp, widx);
   unsigned char* region = lds + u.wave * WAVE_LDS;
   const int p4 = 4 * u.nmy;                 // 16-byte pieces per row in LDS
   const int xm = (u.nmy & 1) ? 3 : 7;       // swizzle mask keeps c ^ (rr & xm) < p4
@@ -974,7 +998,7 @@ __device__ __forceinline__ void run_unit_dma_chunked(const LayerArgs& a, const R
 // ring fill of weights is issued before the expert's rows are gathered.
 template <int TIER, bool BF, int PH, int NT>
 __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& rt, int e, int blk,
-                                              int sp, int tile, unsigned char* lds) {
+                                              int sp, int tile, unsigned char* lds, int widx = -1) {
   using G = Geo<TIER, PH, NT>;
   constexpr int RS = G::RS, QPK = G::QPK, P = G::P;
   // BF16 and INT8 down units take their 64 rows in two passes of 32, so that
@@ -982,7 +1006,7 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
   constexpr int RSP = (TIER != 2 && PH == 1) ? RS / 2 : RS;  // row sets per pass
   constexpr int NPASS = RS / RSP;
   using pass0_t = std::integral_constant<int, 0>;
-  const UnitCtx<TIER, PH, NT> u(a, e, blk, sp);
+  const UnitCtx<TIER, PH, NT> u(a, e, blk, sp, widx);
   int voff[RS];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs)
@@ -1194,9 +1218,11 @@ __global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
     for (int i = blockIdx.x * DNT + threadIdx.x; i <= kDecodeMaxHBlocks; i += gridDim.x * DNT)
       __hip_atomic_store(sync_c(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  // mixed banks: every expert's (tier << 16) | row, behind the row counts
+  int* emap = reinterpret_cast<int*>(cntw + ((a.Ep + 1) >> 1));
   uint32_t word;
   int incl, c;
-  const int n_active = route(a, rt, cntw, word, incl, c);
+  const int n_active = route<MIXED>(a, rt, cntw, word, incl, c, emap);
   if (n_active == 0) {  // nothing routed: the output is zero
     if (PH == 1) {
       uint4* o = reinterpret_cast<uint4*>(a.out);
@@ -1238,21 +1264,23 @@ __global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     int e, blk, sp, t;
     decode(u, e, blk, sp, t);
-    const int tier = MIXED ? __builtin_amdgcn_readfirstlane((int)a.tier[e]) : 2;
+    const int ev = MIXED ? __builtin_amdgcn_readfirstlane(emap[e]) : (2 << 16);
+    const int tier = ev >> 16;
+    const int widx = MIXED ? (ev & 0xffff) : -1;
     if (!MIXED || tier == 2) {
       if constexpr (PATH == 1 && NT == 1 && !MIXED)
         run_unit_kb<BF, PH>(a, rt, e, blk, sp, t, n_units > 2 * (int)gridDim.x);
       else if constexpr (PATH == 1)
-        run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
+        run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
       else if constexpr (PATH == 2 && PH == 0)
         run_unit_dma_chunked<BF, NT>(a, rt, e, blk, t, dyn_lds);
       else
-        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
+        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
     } else if constexpr (MIXED) {
       if (tier == 1)
-        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
+        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
       else
-        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds);
+        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
     }
     if constexpr (PH == 1)
       if (a.combine) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_tiles, &s_flag);
@@ -1859,7 +1887,8 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
       return check_launch("decode_down_rows_kernel");
     }
     // per-wave weight slices / partial tiles, then the per-expert row counts
-    const size_t lds = (size_t)DW * WAVE_LDS + (((size_t)(d.Ep + 1) / 2 * 4 + 15) & ~(size_t)15);
+    const size_t lds = (size_t)DW * WAVE_LDS + (((size_t)(d.Ep + 1) / 2 * 4 + 15) & ~(size_t)15) +
+                       (mixed ? (size_t)d.Ep * 4 : 0);  // (+ the mixed bank's expert map)
     if (ph == 1) {
       // Few down units (large experts, few active): split each (expert, row
       // block) contraction over up to kDecodeMaxSplit work-groups, each with
