@@ -137,6 +137,9 @@ __device__ __forceinline__ int* sync_done(const LayerArgs& a) {
   return a.sync + (kDecodeMaxBuckets + kDecodeMaxHBlocks) * SYNC_INTS;
 }
 
+// Row field of a mixed bank's expert map entry (tier in the top two bits).
+constexpr uint32_t kRowMask = 0x3fffffffu;
+
 // The batch's routed ids and active-expert bitmap, per work-group.
 struct Route {
   uint32_t bitmap[MAX_BM_WORDS];
@@ -149,8 +152,10 @@ struct Route {
 // select_expert.
 // Also counts each expert's rows into cntw (16 bits per expert, two per word;
 // a count is at most T * k <= MAX_SLOTS, so no carry crosses a half).
-// MAP (mixed banks): also writes emap[e] = (tier << 16) | row of expert e in
-// its tier's bank, for every expert, from loads issued beside the id loads.
+// MAP (mixed banks): also writes emap[e] = (tier << 30) | row of expert e in
+// its tier's bank, for every expert, from loads issued beside the id loads
+// (tier 0 / 1 / 2 in the top two bits; a row below 2^30 in the rest: a bank of
+// 2^30 experts would not fit any GPU's memory).
 template <bool MAP = false>
 __device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t* cntw, uint32_t& word,
                                      int& incl, int& c, int* emap = nullptr) {
@@ -190,7 +195,8 @@ __device__ __forceinline__ int route(const LayerArgs& a, Route& r, uint32_t* cnt
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
       const int e = threadIdx.x + i * DNT;
-      if (e < a.Ep) emap[e] = (int)((mt[i] << 16) | (a.index ? mi[i] : (uint32_t)e));
+      if (e < a.Ep)
+        emap[e] = (int)(((mt[i] & 3u) << 30) | ((a.index ? mi[i] : (uint32_t)e) & kRowMask));
     }
   }
 #pragma unroll
@@ -1218,7 +1224,7 @@ __global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
     for (int i = blockIdx.x * DNT + threadIdx.x; i <= kDecodeMaxHBlocks; i += gridDim.x * DNT)
       __hip_atomic_store(sync_c(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // mixed banks: every expert's (tier << 16) | row, behind the row counts
+  // mixed banks: every expert's (tier << 30) | row, behind the row counts
   int* emap = reinterpret_cast<int*>(cntw + ((a.Ep + 1) >> 1));
   uint32_t word;
   int incl, c;
@@ -1264,9 +1270,9 @@ __global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     int e, blk, sp, t;
     decode(u, e, blk, sp, t);
-    const int ev = MIXED ? __builtin_amdgcn_readfirstlane(emap[e]) : (2 << 16);
-    const int tier = ev >> 16;
-    const int widx = MIXED ? (ev & 0xffff) : -1;
+    const uint32_t ev = MIXED ? (uint32_t)__builtin_amdgcn_readfirstlane(emap[e]) : (2u << 30);
+    const int tier = (int)(ev >> 30);
+    const int widx = MIXED ? (int)(ev & kRowMask) : -1;
     if (!MIXED || tier == 2) {
       if constexpr (PATH == 1 && NT == 1 && !MIXED)
         run_unit_kb<BF, PH>(a, rt, e, blk, sp, t, n_units > 2 * (int)gridDim.x);

@@ -9,7 +9,8 @@
 // GPU's array: calls that overlap on one GPU (two streams, two threads) race
 // on it.  The array keeps the last call's contents; the only part that must
 // start at zero, the decode kernels' combine counters, is cleared by each
-// call's first kernel (as for any caller workspace).
+// call's first kernel (as for any caller workspace).  The first call on a
+// device must be made outside graph capture; later calls may be captured.
 #include "exq_internal.h"
 
 #include <mutex>
@@ -25,13 +26,26 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
 // Device address of this device's scratch array (looked up once per device,
-// with that device current).
-int scratch_address(void** out) {
+// with that device current).  The first lookup on a device may load the code
+// object that holds the array, which places the array in device memory, so it
+// is refused while `s` is being captured into a graph: the caller makes one
+// call outside capture first (a call with n_tokens = 0 is enough).
+int scratch_address(hipStream_t s, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return set_error(EXQ_ERROR_HIP, "exq_moe_int4_fused_forward_noalloc: no usable current device");
   std::lock_guard<std::mutex> g(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t qe = hipStreamIsCapturing(s, &cs);
+    if (qe != hipSuccess || cs != hipStreamCaptureStatusNone) {
+      (void)hipGetLastError();  // a failed query must not be reported by a later launch check
+      return set_error(EXQ_ERROR_UNSUPPORTED,
+                       "exq_moe_int4_fused_forward_noalloc: the first call on device %d is "
+                       "under graph capture (or its capture state is unknown: %s); make one "
+                       "call outside capture first (n_tokens = 0 is enough)",
+                       dev, hipGetErrorString(qe));
+    }
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
@@ -62,10 +76,12 @@ extern "C" int exq_moe_int4_fused_forward_noalloc(
                      "%s: this problem needs %zu bytes of scratch; the no-alloc entry point "
                      "holds %zu (use exq_moe_int4_fused_forward with a workspace)",
                      fn, need, (size_t)EXQ_NOALLOC_SCRATCH_BYTES);
-  if (problem->n_tokens == 0) return EXQ_SUCCESS;
+  // the scratch address is resolved even for an empty batch, so that a call with
+  // n_tokens = 0 prepares a device for later calls under graph capture
   void* ws = nullptr;
-  const int st = scratch_address(&ws);
+  const int st = scratch_address(as_stream(stream), &ws);
   if (st) return st;
+  if (problem->n_tokens == 0) return EXQ_SUCCESS;
   return exq_moe_int4_fused_forward(problem, hidden, topk_ids, topk_weights, w13_packed,
                                     w13_scales, w2_packed, w2_scales, out, sort_order_out,
                                     expert_ends_out, ws, (size_t)EXQ_NOALLOC_SCRATCH_BYTES,

@@ -122,6 +122,16 @@ __device__ __forceinline__ void store1(void* out, int dtype, int64_t i, float v)
     reinterpret_cast<uint16_t*>(out)[i] = (uint16_t)f32_to_f16_bits(v);
 }
 
+// Maximum and clamp that keep NaN, as torch's amax and clamp do (quant_shim.py:
+// 92-95): a NaN or infinite weight makes its whole row (INT8) or group (INT4)
+// NaN.  fmaxf / fminf alone would return the other operand.
+__device__ __forceinline__ float max_keep_nan(float a, float b) {
+  return __builtin_isnan(a) ? a : (__builtin_isnan(b) ? b : fmaxf(a, b));
+}
+__device__ __forceinline__ float clamp_keep_nan(float v, float lo, float hi) {
+  return __builtin_isnan(v) ? v : fminf(fmaxf(v, lo), hi);
+}
+
 // Fake quantisation (quantise then dequantise in place of the weights):
 // INT4 per group of g along the row (a short last group counts as padded with
 // zeros), INT8 per row; out = q * scale with the fp32 scale, in the weights'
@@ -139,11 +149,11 @@ __global__ void __launch_bounds__(256) fake_int4_kernel(const void* w, int dtype
   const int k1 = k0 + g < K ? k0 + g : K;
   const int64_t base = row * K;
   float m = 0.f;
-  for (int k = k0 + lane; k < k1; k += 64) m = fmaxf(m, fabsf(load1(w, dtype, base + k)));
-  for (int d = 1; d < 64; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
-  const float scale = fmaxf(m / 7.0f, kFp32Eps);
+  for (int k = k0 + lane; k < k1; k += 64) m = max_keep_nan(m, fabsf(load1(w, dtype, base + k)));
+  for (int d = 1; d < 64; d <<= 1) m = max_keep_nan(m, __shfl_xor(m, d, 64));
+  const float scale = max_keep_nan(m / 7.0f, kFp32Eps);
   for (int k = k0 + lane; k < k1; k += 64) {
-    const float q = fminf(fmaxf(rintf(load1(w, dtype, base + k) / scale), -8.f), 7.f);
+    const float q = clamp_keep_nan(rintf(load1(w, dtype, base + k) / scale), -8.f, 7.f);
     store1(out, dtype, base + k, q * scale);
   }
 }
@@ -153,14 +163,15 @@ __global__ void __launch_bounds__(256) fake_int8_kernel(const void* w, int dtype
   __shared__ float red[4];
   const int64_t base = (int64_t)blockIdx.x * K;
   float m = 0.f;
-  for (int k = threadIdx.x; k < K; k += blockDim.x) m = fmaxf(m, fabsf(load1(w, dtype, base + k)));
-  for (int d = 1; d < 64; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  for (int k = threadIdx.x; k < K; k += blockDim.x)
+    m = max_keep_nan(m, fabsf(load1(w, dtype, base + k)));
+  for (int d = 1; d < 64; d <<= 1) m = max_keep_nan(m, __shfl_xor(m, d, 64));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float scale = fmaxf(m / 127.0f, kFp32Eps);
+  m = max_keep_nan(max_keep_nan(red[0], red[1]), max_keep_nan(red[2], red[3]));
+  const float scale = max_keep_nan(m / 127.0f, kFp32Eps);
   for (int k = threadIdx.x; k < K; k += blockDim.x) {
-    const float q = fminf(fmaxf(rintf(load1(w, dtype, base + k) / scale), -128.f), 127.f);
+    const float q = clamp_keep_nan(rintf(load1(w, dtype, base + k) / scale), -128.f, 127.f);
     store1(out, dtype, base + k, q * scale);
   }
 }

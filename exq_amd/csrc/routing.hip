@@ -465,10 +465,16 @@ __device__ __forceinline__ float key_logit(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// One wave per token: lane l holds logits l, l + 64, ...  Each of the k rounds
-// takes the largest remaining logit (equal logits: the lower id) with one DPP
-// maximum over the lanes' best keys, and a DPP minimum over the ids only when
-// several lanes hold that key.
+// One wave per token: lane l holds logits l, l + 64, ...  The ranking is the
+// reference's, torch.topk over the fp32 softmax (triton_emitter.py:273-277):
+// every expert's probability p = exp(l - max) / sum is computed first (IEEE
+// division, as numpy's and torch's `/`), and each of the k rounds takes the
+// largest remaining p, equal p to the lower id.  Two different logits whose
+// probabilities round to the same fp32 value are a tie, exactly as in the
+// reference; ranking on the logits would split it.  A round is one DPP maximum
+// over the lanes' best keys, plus a DPP minimum over the ids only when several
+// lanes hold that key.  Key = bits(p) + 1 (p >= 0, so the bits are ordered);
+// key 0 marks an expert that is taken or absent.
 template <int MAXC>
 __global__ void __launch_bounds__(256) topk_softmax_kernel(const void* logits, int ldt, int T,
                                                           int E, int k, int renorm, void* ids,
@@ -487,11 +493,17 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(const void* logits, i
     kmax = umax(kmax, key[c]);
   }
   const float m = key_logit(wave_reduce_u32<0u>(kmax, umax));
+  float ex[MAXC];
   float sum = 0.f;
 #pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    ex[c] = lane + 64 * c < E ? expf(key_logit(key[c]) - m) : 0.f;
+    sum += ex[c];
+  }
+  const float S = wave_sum_f32(sum);
+#pragma unroll
   for (int c = 0; c < MAXC; ++c)
-    if (lane + 64 * c < E) sum += expf(key_logit(key[c]) - m);
-  const float inv = 1.0f / wave_sum_f32(sum);
+    key[c] = lane + 64 * c < E ? __float_as_uint(ex[c] / S) + 1u : 0u;
   float mine = 0.f;  // lane j < k: weight of the j-th choice
   int my_id = 0;     // lane j < k: id of the j-th choice
   float ws = 0.f;    // sum of the chosen weights, in choice order
@@ -518,7 +530,7 @@ __global__ void __launch_bounds__(256) topk_softmax_kernel(const void* logits, i
       for (int c = 0; c < MAXC; ++c)
         if (c == (be >> 6)) key[c] = 0u;
     }
-    const float w = expf(key_logit(K) - m) * inv;
+    const float w = __uint_as_float(K - 1u);
     ws += w;
     if (lane == j) {
       mine = w;

@@ -184,6 +184,22 @@ class MixedExpertBank:
     int4_w2_scales: torch.Tensor | None = None
     _keep: list = field(default_factory=list, repr=False)
 
+    def __post_init__(self):
+        # The kernels read tier / index on the device unchecked (tier in the top
+        # two bits of a 32-bit entry, the row in the other 30), so the values
+        # are checked once here, when the bank is built.
+        n = self.n_experts + self.n_shared
+        if self.tier.numel() != n or self.index.numel() != n:
+            raise ValueError(f"tier and index need {n} entries (routed + shared experts)")
+        if self.tier.dtype != torch.int8 or self.index.dtype != torch.int32:
+            raise ValueError("tier must be int8 and index int32")
+        t = self.tier.cpu()
+        i = self.index.cpu()
+        if n and not bool(((t >= 0) & (t <= 2)).all()):
+            raise ValueError("tier values must be 0 (BF16), 1 (INT8) or 2 (INT4)")
+        if n and not bool(((i >= 0) & (i < (1 << 30))).all()):
+            raise ValueError("index values must be bank rows in [0, 2^30)")
+
     @classmethod
     def from_weights(cls, w13: torch.Tensor, w2: torch.Tensor, tiers, *,
                      act_dtype: torch.dtype = torch.bfloat16, group_size: int = 128,

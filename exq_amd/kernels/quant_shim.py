@@ -13,7 +13,13 @@ from .. import _lib
 def _fake(weight: torch.Tensor, bits: int, group_size: int) -> torch.Tensor:
     w = weight.contiguous()
     dev = _lib.require_gpu(w)
-    if w.dim() == 0 or w.numel() == 0:
+    if w.dim() == 0:
+        # quant_shim.py:90-96 reduces a 0-dim tensor over dim -1 as one element;
+        # quant_shim.py:108 indexes shape[-1], which raises for 0-dim input
+        if bits == 4:
+            raise IndexError("quantize_tensor_int4: a 0-dim tensor has no last dimension")
+        return _fake(w.reshape(1), bits, group_size).reshape(())
+    if w.numel() == 0:
         return w.clone()
     K = w.shape[-1]
     rows = w.numel() // K

@@ -237,7 +237,11 @@ typedef struct exq_moe_problem {
 
 /*
  * Weight banks of a mixed-precision layer.  tier[e] / index[e] (device
- * arrays of n_experts + n_shared entries) select the bank and the row in it.
+ * arrays of n_experts + n_shared entries) select the bank and the row in it:
+ * tier[e] must be 0, 1 or 2 and index[e] a row of that tier's bank, in
+ * [0, 2^30).  The arrays live on the device, so the library does not check
+ * them; other values make the layer read outside the banks (the Python
+ * MixedExpertBank checks them when it is built).
  * BF16 bank: weights in the activation dtype.  INT8 bank: int8 weights with
  * one fp16 scale per output row (quant_shim.py:84-96 semantics).  INT4 bank:
  * the packed layout above.
@@ -318,8 +322,11 @@ int exq_moe_mixed_forward(const exq_moe_problem* problem, const void* hidden,
  * nothing (no hipMalloc / hipFree).  Every call on one GPU shares that GPU's
  * scratch, so calls that may overlap on one GPU (other streams, other
  * threads) race: serialise them.  Nothing in the scratch needs to start at
- * zero (the layer's first kernel clears its counters).  Same arguments and
- * results otherwise.
+ * zero (the layer's first kernel clears its counters).  The first call on a
+ * device looks the scratch up and must be made outside graph capture (under
+ * capture it returns EXQ_ERROR_UNSUPPORTED and launches nothing); a call with
+ * n_tokens = 0 is enough, and later calls may be captured and replayed.  Same
+ * arguments and results otherwise.
  */
 #define EXQ_NOALLOC_SCRATCH_BYTES (64u << 20)
 int exq_moe_int4_fused_forward_noalloc(const exq_moe_problem* problem, const void* hidden,

@@ -132,9 +132,14 @@ def dequant_int8(q: np.ndarray, scales: np.ndarray) -> np.ndarray:
 def fake_quant_int8(weights: np.ndarray) -> np.ndarray:
     """quant_shim.py:84-96 verbatim semantics (fp32 scale, output in input dtype).
 
-    pinned by: the reference's zero-row known answer (test_eval.py:158-163).
+    pinned by: the reference's zero-row known answer (test_eval.py:158-163) and
+    hand-derived answers with four distinct per-row scales (one exact in fp32
+    but not in fp16, one set by the fp32-eps clamp) and half-way ties
+    (tests/test_oracle_quant.py::test_fake_quant_int8_known_answers_per_row_scales).
     """
     w = np.asarray(weights)
+    if w.ndim == 0:  # torch reduces a 0-dim tensor over dim -1 as one element
+        return fake_quant_int8(w.reshape(1)).reshape(())
     w32 = w.astype(np.float32)
     scale = np.maximum(np.abs(w32).max(axis=-1, keepdims=True) / np.float32(127.0), FP32_EPS)
     q = np.clip(np.rint(w32 / scale), -128, 127)
@@ -149,6 +154,8 @@ def fake_quant_int4(weights: np.ndarray, group_size: int = 128) -> np.ndarray:
     """
     w = np.asarray(weights)
     shape = w.shape
+    if w.ndim == 0:  # quant_shim.py:108 reads shape[-1]
+        raise IndexError("fake_quant_int4: a 0-dim array has no last dimension")
     w32 = w.astype(np.float32)
     pad = (-shape[-1]) % group_size
     if pad:

@@ -63,3 +63,34 @@ def test_fake_quant_in_place_and_errors(device):
                                     w.data_ptr(), _lib.stream_handle(w.device)), "bits")
     with pytest.raises(_lib.ExqError):
         quantize_tensor_int4(torch.zeros(4, 8))  # host tensor: no host path
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_fake_quant_nan_inf_and_0dim(dtype, device):
+    """torch's amax / clamp keep NaN (quant_shim.py:92-95, 114-117): a NaN or
+    infinite weight turns its whole INT8 row or INT4 group into NaN, and the
+    other rows and groups are untouched.  A 0-dim tensor is one INT8 element;
+    INT4 indexes shape[-1] and raises."""
+    from exq_amd.kernels import quantize_tensor_int4, quantize_tensor_int8
+    banner(f"fake quant NaN / inf / 0-dim {dtype}")
+    w = torch.from_numpy(_weights((2, 6, 256), 3)).to(dtype)
+    w[0, 0, 5] = float("nan")     # row 0, group 0
+    w[0, 2, 200] = float("inf")   # row 2, group 1
+    w[0, 3, 7] = float("-inf")    # row 3, group 0
+    for bits, fn in ((4, quantize_tensor_int4), (8, quantize_tensor_int8)):
+        got = fn(w.to(device)).cpu()
+        ref = torch.from_numpy(_oracle(w.float().numpy(), bits)).to(dtype)
+        assert torch.equal(torch.isnan(got), torch.isnan(ref))
+        fin = ~torch.isnan(ref)
+        assert torch.equal(got[fin], ref[fin])
+        if bits == 8:
+            assert torch.isnan(got[0, [0, 2, 3]]).all() and not torch.isnan(got[0, [1, 4, 5]]).any()
+        else:
+            assert torch.isnan(got[0, 0, :128]).all() and not torch.isnan(got[0, 0, 128:]).any()
+            assert torch.isnan(got[0, 2, 128:]).all() and not torch.isnan(got[0, 2, :128]).any()
+    s = torch.tensor(0.3, dtype=dtype)
+    got = quantize_tensor_int8(s.to(device)).cpu()
+    assert got.shape == () and torch.equal(got, torch.from_numpy(
+        np.asarray(quant.fake_quant_int8(s.float().numpy()))).to(dtype))
+    with pytest.raises(IndexError):
+        quantize_tensor_int4(s.to(device))

@@ -133,8 +133,10 @@ def test_workspace_contents_do_not_matter(device):
     from exq_amd.kernels import fused_experts
     from exq_amd.kernels.fused_moe import moe_workspace_bytes
     gen = torch.Generator(device="cpu").manual_seed(3)
-    # Qwen3 at 1 / 16 / 64 tokens, and a top-2 layer at one token (the gate/up
-    # kernel by output rows before the tiled down kernel's in-kernel combine)
+    # Qwen3 at 1 / 16 / 64 tokens (the rows kernels at one token, the tiled
+    # kernels with the in-kernel combine at 16 and the combine launch at 64), and
+    # a top-2 layer at one token (k < 4: the tiled gate/up and tiled down kernels,
+    # the down kernel's in-kernel combine)
     top2 = synth.MoeConfig("top2", 34, 1024, 512, 8, 2, True, zipf=False)
     for cfg, Ts in ((synth.CONFIGS["qwen3"], (1, 16, 64)), (top2, (1,))):
         p13, s13, p2, s2 = _pack_gpu(cfg.n_experts, cfg.inter, cfg.hidden, synth.seed_for(cfg),

@@ -128,3 +128,48 @@ def test_shared_experts_deepseek_shape(T, device):
                         np.stack([p[1] for p in parts]), np.vectorize(remap.get)(ids), w,
                         np.stack([p[0] for p in sh]), np.stack([p[1] for p in sh]))
     assert_close_rel(out, ref, TOL, f"deepseek shared T={T}")
+
+
+@pytest.mark.parametrize("layer", [0, 1])
+def test_mixed_olmoe_stack_artifact_plan(layer, device, tmp_path):
+    """The mixed stack exactly as the bench times it: tiers from the quant-plan
+    artifact (router-ranked: the router's most frequent 10 % of experts BF16, the
+    next 20 % INT8, the rest INT4; exq_artifact.py:96-192) read back with
+    load_exq_artifact, full OLMoE shape, T = 32.  The hot BF16 experts then hold
+    more than 16 rows (several 16-row tiles); sort_order is bit-exact and the
+    output within 0.5 % of the oracle."""
+    import json
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed, load_exq_artifact
+    from oracle import routing
+    banner(f"mixed olmoe stack, artifact plan, layer {layer}, T=32")
+    cfg = synth.CONFIGS["mixed_olmoe"]
+    path = tmp_path / "plan.json"
+    path.write_text(json.dumps(synth.plan_artifact(cfg, n_layers=2)), encoding="utf-8")
+    plan = load_exq_artifact(str(path), device="cpu")
+    tiers = plan.tiers[layer].tolist()
+    assert tiers == synth.router_tiers(cfg, layer)
+    w13, w2 = synth.expert_weights_gpu(cfg.n_experts, cfg.inter, cfg.hidden,
+                                       synth.seed_for(cfg, layer), device)
+    bank = MixedExpertBank.from_weights(w13, w2, tiers)
+    del w13, w2
+    T = 32
+    ids, w = synth.routing(cfg, T, layer)
+    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
+    bf16 = [e for e in range(cfg.n_experts) if tiers[e] == 0]
+    assert max(counts[bf16]) > 16, "the hot BF16 experts should span several 16-row tiles"
+    x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 99)).to(torch.bfloat16).to(device)
+    so = torch.empty(T * cfg.top_k, dtype=torch.int64, device=device)
+    ends = torch.empty(cfg.n_experts + 1, dtype=torch.int32, device=device)
+    out = fused_experts_mixed(x, bank, torch.from_numpy(w).to(device),
+                              torch.from_numpy(ids).to(device), sort_order_out=so,
+                              expert_ends_out=ends)
+    r_so, r_ends, _ = routing.sort_tokens_by_expert(ids, cfg.n_experts)
+    assert np.array_equal(so.cpu().numpy(), r_so)
+    assert np.array_equal(ends.cpu().numpy(), r_ends)
+    used = np.unique(ids)
+    parts = {int(e): _dequant_bank(bank, int(e)) for e in used}
+    remap = {int(e): i for i, e in enumerate(used)}
+    ref = moe.moe_layer(x.float().cpu().numpy(), np.stack([parts[int(e)][0] for e in used]),
+                        np.stack([parts[int(e)][1] for e in used]),
+                        np.vectorize(remap.get)(ids), w)
+    assert_close_rel(out, ref, TOL, f"mixed olmoe stack artifact plan layer {layer} T=32")

@@ -1,8 +1,8 @@
 """The GPU router (fp32 softmax -> top-k -> optional renormalisation) vs the
-oracle restatement: expert ids bit-exact (descending, equal logits to the
-lower id), weights within 2e-6 relative in fp32 (the kernel's exp and sum
-order differ from numpy's in the last bits) and within bf16 / fp16 rounding
-otherwise.  Covers every config's expert count, E up to 1024, k up to 16,
+oracle restatement: expert ids bit-exact (descending rounded fp32 softmax,
+equal probabilities to the lower id, also where the logits differ), weights
+within 2e-6 relative in fp32 (the kernel's exp and sum order differ from
+numpy's in the last bits) and within bf16 / fp16 rounding otherwise.  Covers every config's expert count, E up to 1024, k up to 16,
 all logit / id / weight dtypes, exact ties, masked (-inf) experts, T = 0 and
 a large T."""
 import numpy as np
@@ -92,3 +92,25 @@ def test_router_masked_experts_and_edges(device):
     assert w0.shape == (0, 4) and ids0.shape == (0, 4)
     big = rng.standard_normal((20000, 128)).astype(np.float32)
     _check(torch.from_numpy(big), 8, True)
+
+
+def test_router_rounded_softmax_ties(device):
+    """The ranking is on the rounded fp32 softmax (torch.topk over F.softmax,
+    triton_emitter.py:273-277): two different logits whose probabilities are
+    bit-equal are a tie, and the lower id goes first, inside the top k and at
+    its last place.  Ranking on the logits would give [0, 2, 1] and [0, 2]."""
+    from exq_amd.kernels import fused_topk
+    from tests.test_oracle_routing import _rounded_softmax_tie_rows
+    banner("router rounded-softmax ties")
+    a_row, b_row, wide = _rounded_softmax_tie_rows()
+    small = torch.from_numpy(np.stack([a_row, b_row]))
+    for k, want in ((3, [[0, 1, 2], [0, 1, 2]]), (2, [[0, 1], [0, 1]])):
+        _, ids = fused_topk(small.cuda(), k, False, ids_dtype=torch.int64)
+        assert ids.cpu().tolist() == want
+        _check(small, k, False)
+        _check(small, k, True)
+    big = torch.from_numpy(np.stack([wide] * 5))
+    _, ids = fused_topk(big.cuda(), 8, False, ids_dtype=torch.int64)
+    assert ids.cpu().tolist() == [[63, 50, 51, 52, 53, 54, 55, 9]] * 5
+    _check(big, 8, False)
+    _check(big, 8, True)

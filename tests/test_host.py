@@ -296,3 +296,21 @@ def test_mixed_plan_hot_tier_is_the_routers_favoured_experts(tmp_path):
         i4 = [e for e in range(64) if tiers[e] == 2]
         # hot experts take far more slots than the INT4 tail on average
         assert counts[bf].mean() > 4 * counts[i4].mean()
+
+
+def test_mixed_bank_checks_tier_and_index_values():
+    """The kernels read tier / index unchecked on the device (the row in 30
+    bits of the expert map), so MixedExpertBank rejects other values when built."""
+    from exq_amd.kernels import MixedExpertBank
+    kw = dict(n_experts=4, n_shared=0, hidden_size=256, inter_size=128, group_size=128)
+    ok = MixedExpertBank(tier=torch.tensor([0, 1, 2, 2], dtype=torch.int8),
+                         index=torch.tensor([0, 0, 0, (1 << 30) - 1], dtype=torch.int32), **kw)
+    assert ok.n_experts == 4
+    for tier, index, msg in (([0, 1, 3, 2], [0, 0, 0, 1], "tier values"),
+                             ([0, 1, -1, 2], [0, 0, 0, 1], "tier values"),
+                             ([0, 1, 2, 2], [0, 0, 0, 1 << 30], "index values"),
+                             ([0, 1, 2, 2], [0, 0, -1, 1], "index values"),
+                             ([0, 1, 2], [0, 0, 0], "entries")):
+        with pytest.raises(ValueError, match=msg):
+            MixedExpertBank(tier=torch.tensor(tier, dtype=torch.int8),
+                            index=torch.tensor(index, dtype=torch.int32), **kw)

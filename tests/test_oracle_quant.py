@@ -161,3 +161,75 @@ def test_dequant_int8_per_row_scales_known_answer():
     ss = np.stack([s, np.array([2.0, 4.0], np.float16)])
     d2 = quant.dequant_int8(qq, ss)
     assert d2[1].tolist() == [[-256.0, 6.0, 0.0], [4.0, -8.0, 508.0]]
+
+
+def test_fake_quant_int8_known_answers_per_row_scales():
+    """quant_shim.py:84-96 on non-zero data, answers derived by hand.
+
+    Every row has its own scale = max|w| / 127 (fp32), and every expected value
+    is q * scale with q an integer, exact in fp32:
+      row 0: scale 1; half-way ties round to even (63.5 -> 64, 2.5 -> 2,
+             -0.5 -> -0, -126.5 -> -126);
+      row 1: scale 1 + 2^-12, exact in fp32 but not in fp16 (fp16 rounds it to
+             1.0, which would give q instead of q * scale);
+      row 2: max|w| = 127 * 2^-24, so max|w| / 127 = 2^-24 is below fp32 eps and
+             the clamp makes the scale 2^-23 (127 * 2^-24 / 2^-23 = 63.5 -> 64);
+      row 3: scale 2^-7.
+    Column 0 holds the largest value of every row and row 0's 127 dominates each
+    column, so a per-column scale fails rows 1-3; a scale kept in fp16 fails row 1;
+    a missing eps clamp or rounding half away from zero fails rows 0 and 2."""
+    s1 = 1.0 + 2.0 ** -12
+    s2 = 2.0 ** -23
+    s3 = 2.0 ** -7
+    w = np.array([
+        [127.0, 63.5, -0.5, 1.5, 2.5, -126.5, 0.0, 5.0],
+        [127 * s1, -3 * s1, 2.5 * s1, 3.5 * s1, -6.5 * s1, 100 * s1, 0.25 * s1, -127 * s1],
+        [127 * 2.0 ** -24, -1 * 2.0 ** -24, 3 * 2.0 ** -24, 0.0, 0.0, 0.0, 0.0, 0.0],
+        [127 * s3, 0.5 * s3, -1.5 * s3, 126.5 * s3, -2 * s3, 7 * s3, -127 * s3, 64 * s3],
+    ], dtype=np.float64)
+    w32 = w.astype(np.float32)
+    assert np.array_equal(w32.astype(np.float64), w)          # inputs exact in fp32
+    want = np.array([
+        [127.0, 64.0, -0.0, 2.0, 2.0, -126.0, 0.0, 5.0],
+        [127 * s1, -3 * s1, 2 * s1, 4 * s1, -6 * s1, 100 * s1, 0.0, -127 * s1],
+        [64 * s2, -0.0, 2 * s2, 0.0, 0.0, 0.0, 0.0, 0.0],
+        [127 * s3, 0.0, -2 * s3, 126 * s3, -2 * s3, 7 * s3, -127 * s3, 64 * s3],
+    ], dtype=np.float64)
+    got = quant.fake_quant_int8(w32)
+    assert got.dtype == np.float32
+    assert np.array_equal(got.astype(np.float64), want)
+    assert np.signbit(got[0, 2]) and np.signbit(got[2, 1])    # rint(-0.5) is -0
+    # the storage form keeps the same integers (scales then rounded to fp16)
+    q, s = quant.quantize_int8(w32)
+    assert q[0].tolist() == [127, 64, 0, 2, 2, -126, 0, 5]
+    assert q[1].tolist() == [127, -3, 2, 4, -6, 100, 0, -127]
+    assert q[2, :3].tolist() == [64, 0, 2]
+    assert s[1] == np.float16(1.0) and s[2] == np.float16(2.0 ** -23)
+    # fp16 and bf16 weights: the result is cast back to the input dtype
+    h = np.array([[127.0, 1.5, -0.5, 2.5, 0.0, 0.0, 0.0, 0.0],
+                  [0.5 * 127 / 128, 0.5 * 2.5 / 128, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0]],
+                 dtype=np.float16)
+    assert quant.fake_quant_int8(h).tolist() == [[127.0, 2.0, -0.0, 2.0, 0.0, 0.0, 0.0, 0.0],
+                                                 [0.5 * 127 / 128, 0.5 * 2 / 128, 0.0, 0.0,
+                                                  0.0, 0.0, 0.0, 0.0]]
+    assert quant.fake_quant_int8(h).dtype == np.float16
+
+
+def test_fake_quant_nan_and_0dim_follow_torch():
+    """torch's amax and clamp keep NaN, so a NaN or infinite weight makes its
+    row (INT8) or group (INT4) NaN; a 0-dim tensor is one INT8 element and
+    makes the INT4 form raise (quant_shim.py:90-96, 108)."""
+    w = np.zeros((3, 256), np.float32)
+    w[:, ::3] = 0.25
+    w[0, 4] = np.nan
+    w[1, 130] = np.inf
+    i8 = quant.fake_quant_int8(w)
+    assert np.isnan(i8[0]).all() and np.isnan(i8[1]).all() and not np.isnan(i8[2]).any()
+    i4 = quant.fake_quant_int4(w)
+    assert np.isnan(i4[0, :128]).all() and not np.isnan(i4[0, 128:]).any()
+    assert np.isnan(i4[1, 128:]).all() and not np.isnan(i4[1, :128]).any()
+    # 0.3 / (0.3 / 127) rounds to 127, and 127 * (0.3 / 127) is 0.3 again in fp32
+    assert quant.fake_quant_int8(np.float32(0.3)) == np.float32(0.3)
+    assert quant.fake_quant_int8(np.float32(0.3)).shape == ()
+    with pytest.raises(IndexError):
+        quant.fake_quant_int4(np.float32(0.3))

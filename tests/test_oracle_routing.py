@@ -123,3 +123,71 @@ def test_align_contract_the_reference_consumer_relies_on(T, k, E, B, seed):
         ent = sorted_ids[blk * B:(blk + 1) * B]
         ent = ent[ent < n]
         assert all(flat[s] == expert_ids[blk] for s in ent)
+
+
+def _rounded_softmax_tie_rows():
+    """Rows whose distinct logits give bit-equal fp32 softmax values.
+
+    0.001 and the next float32 after it differ by 1.2e-10, far below the
+    spacing of float32 near 3.0 (2.4e-7), so l - max rounds to one value for
+    both and their probabilities are equal: a tie that ranking on the logits
+    would split."""
+    a = np.float32(0.001)
+    b = np.nextafter(a, np.float32(1.0))
+    assert a != b
+    rows = [np.array([3.0, a, b, -1.0], np.float32),     # tie inside the top 3
+            np.array([3.0, b, a, -1.0], np.float32)]     # larger logit holds the lower id
+    wide = np.full(64, -5.0, np.float32)                 # tie at the 8th (last) place:
+    wide[50:56] = 2.0                                    # seven clear winners (with 63),
+    wide[9], wide[20] = a, b                             # then 9 and 20 tie
+    wide[63] = 3.0
+    rows.append(wide)
+    return rows
+
+
+@pytest.mark.parametrize("k", [1, 2, 3, 8])
+def test_softmax_topk_matches_torch_on_rounded_ties(k):
+    """The reference routes with torch.topk(F.softmax(logits)) (triton_emitter.py:273-277):
+    the ranking is on the rounded fp32 probabilities, so distinct logits with equal
+    probabilities are a tie.  torch.topk does not fix the order of equal values (on
+    this CPU build, six equal values at ids 50..55 come back as 53 first); the oracle
+    orders a tie by the lower id, a deterministic refinement of torch's result.  So:
+    the chosen probabilities equal torch's bit for bit, a tie is listed in ascending
+    id order, and where torch's ids are unambiguous they are equal."""
+    import torch
+    for row in _rounded_softmax_tie_rows():
+        if k > row.size:
+            continue
+        lg = row[None, :]
+        p = torch.softmax(torch.from_numpy(lg), dim=-1)
+        t_w, t_ids = torch.topk(p, k, dim=-1)
+        ids, w = routing.route_softmax_topk(lg, k, renormalize=False)
+        # torch's exp and its multiply by 1/sum differ from numpy's exp and divide
+        # by a few ulp; the ranking of the rounded values is what must agree
+        np.testing.assert_allclose(w, t_w.numpy(), rtol=1e-6, atol=0)
+        pr = p.numpy()[0]
+        assert ids[0].tolist() == sorted(range(row.size), key=lambda e: (-pr[e], e))[:k]
+        if len(set(pr[ids[0]].tolist())) == k and pr[ids[0][-1]] not in np.delete(pr, ids[0]):
+            assert ids.tolist() == t_ids.numpy().astype(np.int64).tolist()
+    a_row, _, wide = _rounded_softmax_tie_rows()
+    # the 4-expert row: torch's own answer, and the lower id at the k-th place
+    assert routing.route_softmax_topk(a_row[None], 3, False)[0].tolist() == [[0, 1, 2]]
+    assert torch.topk(torch.softmax(torch.from_numpy(a_row[None]), -1), 3)[1].tolist() == [[0, 1, 2]]
+    assert routing.route_softmax_topk(a_row[None], 2, False)[0].tolist() == [[0, 1]]
+    assert routing.route_softmax_topk(wide[None], 8, False)[0].tolist() == [
+        [63, 50, 51, 52, 53, 54, 55, 9]]
+
+
+def test_softmax_topk_matches_torch_on_random_rows():
+    """Ids equal torch.topk over torch's fp32 softmax on seeded rows of every
+    config's width, Zipf-biased and plain."""
+    import torch
+    from exq_amd import synth
+    for name in ("olmoe", "qwen3", "deepseek_v2_lite", "mixtral"):
+        cfg = synth.CONFIGS[name]
+        lg = synth.router_logits(cfg, 256, synth.seed_for(cfg) + 3)
+        p = torch.softmax(torch.from_numpy(lg), dim=-1)
+        tw, t_ids = torch.topk(p, cfg.top_k, dim=-1)
+        ids, w = routing.route_softmax_topk(lg, cfg.top_k, renormalize=False)
+        assert np.array_equal(ids, t_ids.numpy().astype(np.int64))
+        np.testing.assert_allclose(w, tw.numpy(), rtol=2e-6, atol=0)
