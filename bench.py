@@ -42,6 +42,7 @@ import ctypes
 import json
 import os
 import platform
+import subprocess
 import sys
 import time
 
@@ -635,7 +636,15 @@ def stream_read_at_size(dev, nbytes, n_bufs=48, reps=5, grid=2048):
 
 
 def cpu_model():
-    """lscpu-style model name of the host CPU."""
+    """The host CPU's model name as `lscpu` prints it (/proc/cpuinfo otherwise)."""
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10,
+                           env={**os.environ, "LC_ALL": "C"})
+        for line in r.stdout.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -651,19 +660,32 @@ def cpu_threads():
     return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
 
 
+def cpu_counts():
+    """What the host reports beside the threads the baseline uses."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
+    return {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
 def cpu_config_row(name, T, x, routed, shared, tid, tw, cpu):
     """Both variants of the reference CPU path on one configuration's layer:
-    dequantise per call (reference-faithful) and pre-dequantised."""
+    dequantise per call (reference-faithful) and pre-dequantised; plus, for
+    context only, a vectorised per-expert grouping that is not the reference."""
     from oracle.cpu_baseline import time_cpu_experts
     row = {"config": name, "batch": T}
-    for variant in ("dequant_per_call", "predequantized"):
+    for variant in ("dequant_per_call", "predequantized", "grouped"):
         r = time_cpu_experts(x, routed, tid, tw, shared, variant, reps=cpu["reps"], warmup=1,
                              threads=cpu["threads"], budget_s=cpu["budget_s"])
         row[variant] = {"p50_us": round(r["p50_us"], 1), "p5_us": round(r["p5_us"], 1),
                         "p95_us": round(r["p95_us"], 1), "reps": r["reps"],
                         "tokens_per_s": round(T / (r["p50_us"] * 1e-6), 1)}
+    row["grouped"]["label"] = "context only: per-expert grouped matmuls, not the reference"
     log(f"cpu {name} T={T}: {row['dequant_per_call']['p50_us'] / 1e3:.1f} ms "
-        f"(predequantized {row['predequantized']['p50_us'] / 1e3:.1f} ms)")
+        f"(predequantized {row['predequantized']['p50_us'] / 1e3:.1f} ms, "
+        f"grouped {row['grouped']['p50_us'] / 1e3:.1f} ms)")
     return row
 
 
@@ -685,7 +707,9 @@ def cpu_baseline(deq, b, cpu):
                       f"(pytorch_moe_reference loop, torch {torch.__version__} CPU fp32, "
                       f"{cpu['threads']} threads, {cpu_model()})",
             "p5_us": d["p5_us"], "p95_us": d["p95_us"],
-            "predequantized_p50_us": p["p50_us"], "cpu_model": cpu_model()}
+            "predequantized_p50_us": p["p50_us"],
+            "grouped_p50_us_not_reference": row["grouped"]["p50_us"],
+            "cpu_model": cpu_model(), **cpu_counts()}
 
 
 def main():

@@ -12,7 +12,8 @@ Steps (the reference's CPU path, composed into a full layer):
   5. the top-k weighted sum.
 Variant ``"dequant_per_call"`` dequantises the routed experts inside every
 call (reference-faithful); ``"predequantized"`` keeps fp32 weights and times
-the matmuls only.  Mixed-precision banks dequantise each expert by its tier
+the matmuls only; ``"grouped"`` (context only, not the reference) keeps fp32
+weights and multiplies each expert's token rows at once.  Mixed-precision banks dequantise each expert by its tier
 (INT4 as above, INT8 per-row fp16 scale, BF16 widened); always-on shared
 experts are added with weight 1, as the GPU path does.
 
@@ -20,7 +21,8 @@ pinned by: tests/test_oracle_cpu_baseline.py -- ``dequant_int4_torch`` and
 ``dequant_int8_torch`` equal ``oracle.quant.dequant_int4`` / ``dequant_int8``
 bit for bit, and ``moe_layer_loop`` (with and without shared experts) equals
 ``oracle.moe.moe_layer`` (float64) to 1e-5 relative L2, while a dropped top-k
-term or a dropped shared expert misses it by more than 1e-2.
+term or a dropped shared expert misses it by more than 1e-2; ``moe_layer_grouped``
+equals ``moe_layer_loop`` to 1e-5 relative L2.
 """
 from __future__ import annotations
 
@@ -72,6 +74,31 @@ def moe_layer_loop(x: torch.Tensor, w13: dict, w2: dict, ids: torch.Tensor,
     return out
 
 
+def moe_layer_grouped(x: torch.Tensor, w13: dict, w2: dict, ids: torch.Tensor,
+                      wts: torch.Tensor, shared: tuple = ()) -> torch.Tensor:
+    """Vectorised per-expert grouping of the same layer, for context only (NOT
+    the reference's path): each routed expert multiplies all of its token rows
+    at once (one [n_e, H] x [H, 2I] and one [n_e, I] x [I, H] product), and the
+    weighted rows are scattered back with index_add_."""
+    T, k = ids.shape
+    out = torch.zeros(T, x.shape[1], dtype=torch.float32)
+    flat = ids.reshape(-1)
+    for e in sorted(w13):
+        slots = torch.nonzero(flat == e, as_tuple=True)[0]
+        if slots.numel() == 0:
+            continue
+        tok = torch.div(slots, k, rounding_mode="floor")
+        gu = x[tok] @ w13[e].T
+        I = gu.shape[1] // 2
+        y = (torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]) @ w2[e].T
+        out.index_add_(0, tok, y * wts.reshape(-1)[slots].unsqueeze(1))
+    for s13, s2 in shared:
+        gu = x @ s13.T
+        I = gu.shape[1] // 2
+        out += (torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]) @ s2.T
+    return out
+
+
 def time_cpu_experts(x, deq: dict, ids, wts, shared_deq=(), variant: str = "dequant_per_call",
                      reps: int = 20, warmup: int = 1, threads: int | None = None,
                      budget_s: float | None = None) -> dict:
@@ -95,11 +122,12 @@ def time_cpu_experts(x, deq: dict, ids, wts, shared_deq=(), variant: str = "dequ
             w13[e], w2[e] = deq[e]()
         return w13, w2, tuple(f() for f in shared_deq)
 
-    pre = dequant_all() if variant == "predequantized" else None
+    pre = dequant_all() if variant in ("predequantized", "grouped") else None
+    layer = moe_layer_grouped if variant == "grouped" else moe_layer_loop
 
     def run():
         a, b, sh = pre if pre is not None else dequant_all()
-        return moe_layer_loop(x, a, b, ids, wts, sh)
+        return layer(x, a, b, ids, wts, sh)
 
     with torch.no_grad():
         first = None

@@ -125,3 +125,25 @@ def test_budget_caps_reps_for_slow_calls(monkeypatch):
     r = cpu_baseline.time_cpu_experts(t(x), cpu_baseline.int4_deq(t(p13), t(s13), t(p2), t(s2)),
                                       t(ids), t(wts), reps=20, warmup=0, threads=1, budget_s=9)
     assert r["reps"] == 4
+
+
+def test_grouped_variant_equals_loop():
+    """The context-only grouped variant computes the same layer as the
+    reference loop (dropped slots, shared experts and repeated experts too)."""
+    x, p13, s13, p2, s2, ids, wts = _layer(E=5, T=9, k=3, seed=11)
+    ids = ids.copy()
+    ids[2, 1] = -1
+    rng = np.random.default_rng(12)
+    sh13 = torch.from_numpy((rng.standard_normal((1, 256, 256)) * 0.02).astype(np.float32))
+    sh2 = torch.from_numpy((rng.standard_normal((1, 256, 128)) * 0.02).astype(np.float32))
+    d13, d2 = quant.dequant_int4(p13, s13), quant.dequant_int4(p2, s2)
+    w13 = {e: torch.from_numpy(d13[e]) for e in range(5)}
+    w2 = {e: torch.from_numpy(d2[e]) for e in range(5)}
+    t = lambda a: torch.from_numpy(a)  # noqa: E731
+    shared = ((sh13[0], sh2[0]),)
+    a = cpu_baseline.moe_layer_loop(t(x), w13, w2, t(ids), t(wts), shared).numpy()
+    b = cpu_baseline.moe_layer_grouped(t(x), w13, w2, t(ids), t(wts), shared).numpy()
+    assert moe.rel_l2(b, a) < 1e-5
+    r = cpu_baseline.time_cpu_layer(t(x), t(p13), t(s13), t(p2), t(s2), t(ids), t(wts),
+                                    "grouped", reps=3, warmup=1, threads=1)
+    assert r["variant"] == "grouped" and r["reps"] == 3
