@@ -75,6 +75,8 @@ def parse_args():
                     help="calibration copy + one eager pass, for rocprofv3 --pmc")
     ap.add_argument("--pmc-summary", type=str, default="",
                     help="per-kernel mean of a rocprofv3 counter CSV")
+    ap.add_argument("--routing-only", action="store_true",
+                    help="time only the standalone stable sort (exq_dispatch) and exit")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the prefill configurations (DeepSeek-V2-Lite 2048, Mixtral 4096)")
     ap.add_argument("--eager", action="store_true",
@@ -560,7 +562,38 @@ def measure_configs(dev, reps, cpu=None):
         rows.append({"config": "router_qwen3", "batch": T, "experts": cfg.n_experts,
                      "top_k": cfg.top_k, "calls_per_graph": n, "us_per_call": round(ms * 1e3, 2)})
         log(f"config router qwen3 T={T}: {ms * 1e3:.2f} us")
+    rows += routing_rows(dev, reps)
     return rows, north_star, cpu_rows
+
+
+def routing_rows(dev, reps):
+    """The standalone stable sort (exq_dispatch, under sort_tokens_by_expert
+    and moe_grouped_gemm) on seeded DeepSeek-V2-Lite ids: a decode batch (one
+    work-group) and a 2048-token prefill chunk at top-6 and top-8 (12,288 and
+    16,384 slots: the multi-block sort, one launch over 12 / 16 work-groups)."""
+    import torch
+    from exq_amd import synth
+    from exq_amd.kernels.exq_dispatch import dispatch
+    cfg = synth.CONFIGS["deepseek_v2_lite"]
+    rows = []
+    for T, k in ((16, 6), (2048, 6), (2048, 8)):
+        c = synth.MoeConfig("routing", cfg.config_id, cfg.hidden, cfg.inter, cfg.n_experts, k,
+                            False)
+        ids, _ = synth.routing(c, T)
+        t = torch.from_numpy(ids.reshape(-1)).to(dev)
+        n_slots = ids.size
+        so = torch.empty(n_slots, dtype=torch.int64, device=dev)
+        si = torch.empty(n_slots, dtype=torch.int64, device=dev)
+        ends = torch.empty(cfg.n_experts + 1, dtype=torch.int32, device=dev)
+        n = 32  # calls per graph
+        ms = _graph_time(lambda: [dispatch(t, so, si, ends, cfg.n_experts) for _ in range(n)],
+                         reps) / n
+        rows.append({"config": "dispatch_sort", "batch": T, "top_k": k, "slots": n_slots,
+                     "experts": cfg.n_experts, "work_groups": 1 if n_slots <= 2048 else
+                     min(128, -(-n_slots // 1024)), "calls_per_graph": n,
+                     "us_per_call": round(ms * 1e3, 2)})
+        log(f"config dispatch sort {n_slots} slots: {ms * 1e3:.2f} us")
+    return rows
 
 
 def stream_read_ceiling(dev, nbytes=2 << 30, reps=10):
@@ -731,6 +764,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     cfg = synth.CONFIGS["qwen3" if not args.pmc_run else args.config]
+    if args.routing_only:  # the standalone sort alone (profiles)
+        print(json.dumps({"routing": routing_rows(dev, max(5, args.steps // 5))}), flush=True)
+        return
     if args.prefill_only:  # the MFMA-path configurations alone (profiles, counter runs)
         rows = []
         for name in ("deepseek_v2_lite", "mixtral"):

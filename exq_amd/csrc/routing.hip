@@ -1,4 +1,4 @@
-// routing.hip -- routing preparation on one work-group per call.
+// routing.hip -- routing preparation.
 //
 // Decode batches route at most a few thousand slots, so a single 1024-thread
 // work-group does the whole job out of LDS: an LDS-atomic histogram, a
@@ -6,7 +6,10 @@
 // per-bucket slot bitmasks (popcount of the lower bits), so the order inside
 // a bucket is deterministic and ascending -- the canonical order of the
 // reference's stable argsort (exq/kernels/moe_grouped_gemm.py:156-157).
-// Nothing here uses global atomics, hipCUB or temporary allocations.
+// Larger calls run over many work-groups: the fused layer's plan in three
+// launches through its workspace, the standalone entry points in one launch
+// that needs no scratch (each block recounts every item's bucket).  Nothing
+// here uses global atomics, hipCUB or temporary allocations.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -197,6 +200,217 @@ __global__ void __launch_bounds__(RT) align_kernel(const void* ids, int ids_dtyp
   __syncthreads();  // padding fill must land before the scatter overwrites
   stable_scatter(numel, nb, key, s.run, s.masks,
                  [&](int i, int, int pos) { sorted_ids[pos] = i; });
+}
+
+// ---- standalone entry points above one work-group ---------------------------
+// A device-wide stable counting sort that needs no scratch memory: block b owns
+// items [lo, hi) and counts the buckets of ALL n items itself, split into the
+// items before lo and all items.  An exclusive scan of the totals gives every
+// bucket's start; start + (items of the bucket before lo) is where block b's
+// first item of that bucket goes, and a stable scatter of its own items
+// follows.  No block waits for another and nothing is written outside the
+// outputs; the recount costs each block n / RT loads per thread, so the grid
+// is capped at kWideMaxGrid blocks (larger ranges per block past that).
+// Results are identical to the one-work-group kernels (the same stable
+// ascending order inside a bucket).
+constexpr int kWideMaxBuckets = 4096;  // experts + the trailing or shifted bucket
+constexpr int kWideMaxGrid = 128;
+constexpr int kWideVPT = kWideMaxBuckets / RT;  // buckets per thread in the scan
+
+struct WideLds {
+  int tot[kWideMaxBuckets];        // bucket totals over all items
+  int run[kWideMaxBuckets];        // items before lo, then this block's cursors
+  int start[kWideMaxBuckets + 1];  // exclusive starts, start[nb] = total
+  int wsum[RT_WAVES];
+  uint32_t masks[MASK_WORDS];
+};
+
+// tot[] and run[] of block range [lo, ...) over all n items; keys are loaded
+// eight per thread before their LDS atomics, so the loads are in flight together.
+template <typename KeyFn>
+__device__ void wide_count(int n, int lo, int nb, KeyFn key, int* tot, int* before) {
+  for (int b = threadIdx.x; b < nb; b += RT) {
+    tot[b] = 0;
+    before[b] = 0;
+  }
+  __syncthreads();
+  constexpr int U = 8;
+  for (int64_t i0 = 0; i0 < n; i0 += RT * U) {
+    int kv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * RT + (int)threadIdx.x;
+      kv[u] = i < n ? key((int)i) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * RT + (int)threadIdx.x;
+      if (kv[u] >= 0) {
+        atomicAdd(&tot[kv[u]], 1);
+        if (i < lo) atomicAdd(&before[kv[u]], 1);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// start[b] = sum of val(b') for b' < b (b < nb), start[nb] = total; thread t
+// takes buckets t*kWideVPT .. (consecutive), so the order is the bucket order.
+template <typename ValFn>
+__device__ int wide_excl_scan(int nb, ValFn val, int* start, int* wsum) {
+  const int b0 = (int)threadIdx.x * kWideVPT;
+  int loc[kWideVPT];
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < kWideVPT; ++j) {
+    loc[j] = b0 + j < nb ? val(b0 + j) : 0;
+    sum += loc[j];
+  }
+  int total;
+  int ex = block_excl_scan(sum, wsum, &total);
+#pragma unroll
+  for (int j = 0; j < kWideVPT; ++j) {
+    if (b0 + j < nb) start[b0 + j] = ex;
+    ex += loc[j];
+  }
+  if (threadIdx.x == 0) start[nb] = total;
+  __syncthreads();
+  return total;
+}
+
+// Stable scatter of items [lo, hi): item i of bucket b goes to run[b] + (its
+// rank among the range's earlier items of bucket b), in chunks whose per-bucket
+// slot bitmasks fit the mask area; run[] advances after each chunk.
+template <typename KeyFn, typename EmitFn>
+__device__ void wide_scatter(int lo, int hi, int nb, KeyFn key, int* run, uint32_t* masks,
+                             EmitFn emit) {
+  const int tid = threadIdx.x;
+  int wpb = MASK_WORDS / nb;
+  if (wpb > RT / 32) wpb = RT / 32;
+  const int chunk = wpb * 32;
+  for (int base = lo; base < hi; base += chunk) {
+    for (int w = tid; w < nb * wpb; w += RT) masks[w] = 0u;
+    __syncthreads();
+    const int i = base + tid;
+    const int b = (tid < chunk && i < hi) ? key(i) : -1;
+    if (b >= 0) atomicOr(&masks[b * wpb + (tid >> 5)], 1u << (tid & 31));
+    __syncthreads();
+    if (b >= 0) {
+      const uint32_t* m = masks + b * wpb;
+      int r = __popc(m[tid >> 5] & ((1u << (tid & 31)) - 1u));
+      for (int w = 0; w < (tid >> 5); ++w) r += __popc(m[w]);
+      emit(i, b, run[b] + r);
+    }
+    __syncthreads();
+    for (int bb = tid; bb < nb; bb += RT) {
+      int c = 0;
+      for (int w = 0; w < wpb; ++w) c += __popc(masks[bb * wpb + w]);
+      run[bb] += c;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ void __launch_bounds__(RT) wide_dispatch_kernel(const void* ids, int ids_dtype, int n,
+                                                           int E, int per, int64_t* sort_order,
+                                                           int64_t* sorted_ids, int32_t* ends) {
+  __shared__ WideLds s;
+  auto key = [&](int i) -> int {
+    const int64_t v = load_index(ids, ids_dtype, i);
+    return (v >= 0 && v < E) ? (int)v : E;  // ids outside [0, E): trailing bucket E
+  };
+  const int nb = E + 1;
+  const int lo = blockIdx.x * per, hi = min(n, lo + per);
+  wide_count(n, lo, nb, key, s.tot, s.run);
+  wide_excl_scan(nb, [&](int b) { return s.tot[b]; }, s.start, s.wsum);
+  for (int b = threadIdx.x; b < nb; b += RT) s.run[b] += s.start[b];
+  if (blockIdx.x == 0)
+    for (int e = threadIdx.x; e <= E; e += RT) ends[e] = s.start[e];
+  __syncthreads();
+  wide_scatter(lo, hi, nb, key, s.run, s.masks, [&](int i, int, int pos) {
+    sort_order[pos] = i;
+    sorted_ids[pos] = load_index(ids, ids_dtype, i);
+  });
+}
+
+__global__ void __launch_bounds__(RT) wide_build_ends_kernel(const int32_t* sid, int em,
+                                                             const int32_t* fr, int n_active,
+                                                             int E, int per, int32_t* ends,
+                                                             int64_t* sort_order) {
+  __shared__ WideLds s;
+  auto key = [&](int i) -> int {
+    const int slot = sid[i];
+    if (slot < 0 || slot >= n_active) return -1;
+    const int e = fr[slot];
+    return (e >= 0 && e < E) ? e : -1;
+  };
+  const int lo = blockIdx.x * per, hi = min(em, lo + per);
+  wide_count(em, lo, E, key, s.tot, s.run);
+  wide_excl_scan(E, [&](int b) { return s.tot[b]; }, s.start, s.wsum);
+  for (int b = threadIdx.x; b < E; b += RT) s.run[b] += s.start[b];
+  if (blockIdx.x == 0)
+    for (int e = threadIdx.x; e <= E; e += RT) ends[e] = s.start[e];
+  __syncthreads();
+  // a slot listed twice would overflow sort_order; such entries are dropped
+  wide_scatter(lo, hi, E, key, s.run, s.masks, [&](int i, int, int pos) {
+    if (pos < n_active) sort_order[pos] = sid[i];
+  });
+}
+
+__global__ void __launch_bounds__(RT) wide_align_kernel(const void* ids, int ids_dtype, int numel,
+                                                        int nb, int B, int per,
+                                                        int32_t* sorted_ids, int cap,
+                                                        int32_t* expert_ids, int cap_blocks,
+                                                        int32_t* ntpp, int32_t* cumsum, int pad) {
+  __shared__ WideLds s;
+  auto key = [&](int i) -> int {
+    const int64_t v = load_index(ids, ids_dtype, i) + 1;  // bucket 0 holds id == -1
+    return (v >= 0 && v < nb) ? (int)v : -1;
+  };
+  const int lo = blockIdx.x * per, hi = min(numel, lo + per);
+  wide_count(numel, lo, nb, key, s.tot, s.run);
+  const int t = wide_excl_scan(nb, [&](int b) { return ((s.tot[b] + B - 1) / B) * B; }, s.start,
+                               s.wsum);
+  for (int b = threadIdx.x; b < nb; b += RT) s.run[b] += s.start[b];
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i <= nb; i += RT) cumsum[i] = s.start[i];
+    if (threadIdx.x == 0) ntpp[0] = t;
+  }
+  // bucket of padded position p < t: the last bucket whose start is <= p
+  auto bucket_of = [&](int p) {
+    int a = 0, z = nb - 1;
+    while (a < z) {
+      const int mid = (a + z + 1) >> 1;
+      if (s.start[mid] <= p) a = mid; else z = mid - 1;
+    }
+    return a;
+  };
+  const int gtid = blockIdx.x * RT + threadIdx.x, gstride = gridDim.x * RT;
+  for (int blk = gtid; blk < cap_blocks; blk += gstride)
+    expert_ids[blk] = blk * B < t ? bucket_of(blk * B) - 1 : -1;
+  // padding entries only (a bucket's tail past its count, and everything past
+  // t), so no block writes where another block's scatter does
+  if (pad) {
+    for (int p = gtid; p < cap; p += gstride) {
+      bool fill = p >= t;
+      if (!fill) {
+        const int b = bucket_of(p);
+        fill = p - s.start[b] >= s.tot[b];
+      }
+      if (fill) sorted_ids[p] = numel;
+    }
+  }
+  __syncthreads();
+  wide_scatter(lo, hi, nb, key, s.run, s.masks, [&](int i, int, int pos) { sorted_ids[pos] = i; });
+}
+
+// Blocks and items per block of the wide kernels for n items.
+__host__ __forceinline__ void wide_grid(int64_t n, int* grid, int* per) {
+  int64_t g = (n + RT - 1) / RT;
+  if (g > kWideMaxGrid) g = kWideMaxGrid;
+  if (g < 1) g = 1;
+  *grid = (int)g;
+  *per = (int)((n + g - 1) / g);
 }
 
 // ---- fused-path routing plan -----------------------------------------------
@@ -425,10 +639,10 @@ int launch_tg_from_ends(const int32_t* ends, int E, const int32_t* expert_mask, 
 // ---------------------------------------------------------------------------
 // Router: fp32 softmax over a token's expert logits, the top-k experts, and
 // optionally their weights renormalised to sum to one.  One wave per token;
-// lane l holds logits l, l + 64, ...  Softmax is monotonic, so the top-k is
-// taken on the logits themselves (largest first, equal logits to the lower
-// expert id): the ids never depend on how exp() rounds.  The denominator is
-// a fixed-order wave reduction (deterministic).
+// lane l holds logits l, l + 64, ...  The top-k is taken on the rounded fp32
+// probabilities (largest first, equal probabilities to the lower expert id),
+// as torch.topk over the softmax ranks them.  The denominator is a
+// fixed-order wave reduction (deterministic).
 // Wave-wide reductions with DPP (gfx9 row forms): quad swaps, rotations by 4
 // and 8 inside each 16-lane row, then rows folded into row 3 by the row-15 and
 // row-31 broadcasts; lane 63 ends with the result, read back as a scalar.
@@ -556,11 +770,19 @@ extern "C" int exq_dispatch(const void* router_indices, int ids_dtype, int64_t n
                             int32_t* expert_ends, exq_stream stream) {
   EXQ_REQUIRE(is_index_dtype(ids_dtype), "exq_dispatch: ids dtype must be i32 or i64");
   EXQ_REQUIRE(n >= 0 && n <= INT32_MAX, "exq_dispatch: n=%lld out of range", (long long)n);
-  EXQ_REQUIRE(n_experts >= 1 && n_experts < MAX_BUCKETS,
+  EXQ_REQUIRE(n_experts >= 1 && n_experts < kWideMaxBuckets,
               "exq_dispatch: n_experts=%lld must be in [1, %d)", (long long)n_experts,
-              MAX_BUCKETS);
+              kWideMaxBuckets);
   EXQ_REQUIRE(expert_ends && (n == 0 || (router_indices && sort_order && sorted_expert_ids)),
               "exq_dispatch: null pointer");
+  if (n > kRoutePlanOneBlock || n_experts + 1 > MAX_BUCKETS) {
+    int grid, per;
+    wide_grid(n, &grid, &per);
+    hipLaunchKernelGGL(wide_dispatch_kernel, dim3(grid), dim3(RT), 0, as_stream(stream),
+                       router_indices, ids_dtype, (int)n, (int)n_experts, per, sort_order,
+                       sorted_expert_ids, expert_ends);
+    return check_launch("wide_dispatch_kernel");
+  }
   hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(RT), 0, as_stream(stream), router_indices,
                      ids_dtype, (int)n, (int)n_experts, sort_order, sorted_expert_ids,
                      expert_ends);
@@ -573,11 +795,19 @@ extern "C" int exq_build_ends_from_slots(const int32_t* sorted_slot_ids, int64_t
                                          int64_t* sort_order, exq_stream stream) {
   EXQ_REQUIRE(em >= 0 && em <= INT32_MAX && n_active >= 0 && n_active <= INT32_MAX,
               "exq_build_ends_from_slots: sizes out of range");
-  EXQ_REQUIRE(n_experts >= 1 && n_experts <= MAX_BUCKETS,
+  EXQ_REQUIRE(n_experts >= 1 && n_experts <= kWideMaxBuckets,
               "exq_build_ends_from_slots: n_experts=%lld must be in [1, %d]",
-              (long long)n_experts, MAX_BUCKETS);
+              (long long)n_experts, kWideMaxBuckets);
   EXQ_REQUIRE(expert_ends && (em == 0 || (sorted_slot_ids && flat_router && sort_order)),
               "exq_build_ends_from_slots: null pointer");
+  if (em > kRoutePlanOneBlock || n_experts > MAX_BUCKETS) {
+    int grid, per;
+    wide_grid(em, &grid, &per);
+    hipLaunchKernelGGL(wide_build_ends_kernel, dim3(grid), dim3(RT), 0, as_stream(stream),
+                       sorted_slot_ids, (int)em, flat_router, (int)n_active, (int)n_experts, per,
+                       expert_ends, sort_order);
+    return check_launch("wide_build_ends_kernel");
+  }
   hipLaunchKernelGGL(build_ends_kernel, dim3(1), dim3(RT), 0, as_stream(stream),
                      sorted_slot_ids, (int)em, flat_router, (int)n_active, (int)n_experts,
                      expert_ends, sort_order);
@@ -592,9 +822,9 @@ extern "C" int exq_moe_align_block_size(const void* topk_ids, int ids_dtype, int
                                         int pad_sorted_token_ids, exq_stream stream) {
   EXQ_REQUIRE(is_index_dtype(ids_dtype), "exq_moe_align_block_size: ids dtype must be i32/i64");
   EXQ_REQUIRE(numel >= 0 && numel <= INT32_MAX, "exq_moe_align_block_size: numel out of range");
-  EXQ_REQUIRE(num_experts >= 1 && num_experts <= MAX_BUCKETS,
+  EXQ_REQUIRE(num_experts >= 1 && num_experts <= kWideMaxBuckets,
               "exq_moe_align_block_size: num_experts=%lld must be in [1, %d]",
-              (long long)num_experts, MAX_BUCKETS);
+              (long long)num_experts, kWideMaxBuckets);
   EXQ_REQUIRE(block_size >= 1 && block_size <= 4096,
               "exq_moe_align_block_size: block_size=%lld out of range", (long long)block_size);
   const int64_t need = numel + num_experts * (block_size - 1);
@@ -607,6 +837,16 @@ extern "C" int exq_moe_align_block_size(const void* topk_ids, int ids_dtype, int
   EXQ_REQUIRE(sorted_token_ids && expert_ids && num_tokens_post_pad && cumsum &&
                   (numel == 0 || topk_ids),
               "exq_moe_align_block_size: null pointer");
+  if (numel > kRoutePlanOneBlock || num_experts > MAX_BUCKETS) {
+    int grid, per;
+    wide_grid(numel, &grid, &per);
+    hipLaunchKernelGGL(wide_align_kernel, dim3(grid), dim3(RT), 0, as_stream(stream), topk_ids,
+                       ids_dtype, (int)numel, (int)num_experts, (int)block_size, per,
+                       sorted_token_ids, (int)sorted_capacity, expert_ids,
+                       (int)expert_ids_capacity, num_tokens_post_pad, cumsum,
+                       pad_sorted_token_ids ? 1 : 0);
+    return check_launch("wide_align_kernel");
+  }
   hipLaunchKernelGGL(align_kernel, dim3(1), dim3(RT), 0, as_stream(stream), topk_ids, ids_dtype,
                      (int)numel, (int)num_experts, (int)block_size, sorted_token_ids,
                      (int)sorted_capacity, expert_ids, (int)expert_ids_capacity,

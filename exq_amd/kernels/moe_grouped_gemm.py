@@ -84,8 +84,9 @@ def unsort_output(sorted_output: torch.Tensor, router_indices: torch.Tensor,
     Returns ``[n_tokens, N]`` in ``sorted_output``'s dtype.  The inverse
     permutation comes from the same stable dispatch sort as
     ``moe_grouped_gemm`` (so the two compose), with no device->host read:
-    ``n_experts`` bounds the ids (default 1023, the dispatch kernel's largest
-    bucket count); ids in ``[0, n_experts)`` give exactly the reference's
+    ``n_experts`` bounds the ids (default 1023, the largest expert count the
+    one-work-group sort takes; up to 4095 with the multi-block sort); ids in
+    ``[0, n_experts)`` give exactly the reference's
     ``torch.argsort(ids, stable=True)`` order.
     """
     dev = _lib.require_gpu(sorted_output, router_indices, router_weights)

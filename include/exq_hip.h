@@ -71,9 +71,12 @@ const char* exq_status_name(int status);
  * runs before dispatch (exq/codegen/triton_emitter.py:273-277: F.softmax over
  * the router logits, torch.topk, weights divided by their sum), whose output
  * the SGLang hook receives as dispatch_output.topk_output
- * (exq/runtime/sglang_backend.py:88-90).  Softmax in fp32; experts in
- * descending order, equal logits to the lower id; renormalize != 0 divides
- * the k weights by their sum.  E <= 1024, 1 <= k <= min(E, 64).
+ * (exq/runtime/sglang_backend.py:88-90).  Softmax in fp32 (exp(l - max)
+ * divided by the sum with IEEE division); experts in descending order of that
+ * rounded probability, equal probabilities to the lower id (also where the
+ * logits differ: the ranking is torch.topk's over the softmax values);
+ * renormalize != 0 divides the k weights by their sum.  E <= 1024,
+ * 1 <= k <= min(E, 64).
  */
 int exq_topk_softmax(const void* logits, int logits_dtype, int64_t n_tokens,
                      int64_t n_experts, int64_t top_k, int renormalize, void* topk_ids,
@@ -88,7 +91,9 @@ int exq_topk_softmax(const void* logits, int logits_dtype, int64_t n_tokens,
  * inside a bucket is arbitrary) and, if pad_sorted_token_ids, `numel` in
  * every padding entry; expert_ids[blk] = b - 1 for the blocks of bucket b and
  * -1 past the end.  Capacities must be at least numel + num_experts*(B-1)
- * and ceil(that / B); cumsum has num_experts + 1 entries.
+ * and ceil(that / B); cumsum has num_experts + 1 entries.  num_experts <=
+ * 4096.  One work-group up to 2048 ids and 1024 buckets; larger calls run
+ * over several work-groups with the same results and no scratch memory.
  */
 int exq_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
                              int64_t num_experts, int64_t block_size,
@@ -105,6 +110,8 @@ int exq_moe_align_block_size(const void* topk_ids, int ids_dtype, int64_t numel,
  * routed to experts <= e; sort_order[expert_ends[e] + r] = r-th valid slot of
  * expert e in order of appearance (the reference's atomic-cursor order is
  * arbitrary; this one is deterministic).  No pre-zeroing needed.
+ * n_experts <= 4096; above 2048 entries or 1024 experts it runs over several
+ * work-groups (same results, no scratch memory).
  */
 int exq_build_ends_from_slots(const int32_t* sorted_slot_ids, int64_t em,
                               const int32_t* flat_router, int64_t n_active,
@@ -115,6 +122,10 @@ int exq_build_ends_from_slots(const int32_t* sorted_slot_ids, int64_t em,
  * Stable token->expert sort.  Replaces exq_dispatch_cuda.dispatch
  * (exq_dispatch.cu:99-149, bound at :313) and the device half of
  * sort_tokens_by_expert (exq/kernels/moe_grouped_gemm.py:153-163).
+ * n_experts < 4096; ids outside [0, n_experts) sort after every valid id, in
+ * slot order.  Up to 2048 ids and 1023 experts one work-group; larger calls
+ * run over several work-groups (each recounts every id's bucket, so no
+ * scratch memory is needed) with the same results.
  */
 int exq_dispatch(const void* router_indices, int ids_dtype, int64_t n, int64_t n_experts,
                  int64_t* sort_order, int64_t* sorted_expert_ids, int32_t* expert_ends,
