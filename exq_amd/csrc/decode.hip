@@ -121,6 +121,7 @@ struct LayerArgs {
   float* part;                  // [T * kp, H] fp32
   uint16_t* out;                // [T, H]
   int* sync;                    // combine counters, see sync_* below
+  int* plan;                    // per-tile records for the down kernel, see kPlan* below
   int nbA, nbB;                 // units per expert: I / 16, H / rows_b(NT)
   int nsplit;                   // down: k-splits per (expert, row block), partial sets
   int combine;                  // down: 1 = the last unit of a column block combines it,
@@ -328,6 +329,43 @@ __device__ __forceinline__ int lane_slots(const LayerArgs& a, const Route& r, in
   return cnt;
 }
 
+// The down kernel's plan, written by the gate/up kernel of the same call
+// (which has routed already): int plan[0] = the number of 16-row tiles, bit s
+// of the words from plan[kPlanMaskOff] on = routed slot s (t * k + j) has an id
+// in [0, E), then from int kPlanHdrInts on one 32-int (128-byte) record per
+// tile, in unit order:
+//   [0] expert | (tile << 16), [1] the expert's row count, [2] its mixed-bank
+//   map entry (tier << 30 | row), [16 + r] the slot of the tile's row r
+//   (tile * 16 + r, the last row past the count).
+// A down unit then needs one load of its record before its weight copies go
+// out, instead of routing again (loading every id, LDS histogram, barriers).
+constexpr int kPlanHdrInts = 96;   // [0] tile count; [32, 66) the routed slots' validity bits
+constexpr int kPlanMaskOff = 32;
+constexpr int kPlanRecInts = 32;
+constexpr int kPlanSlotOff = 16;
+static_assert(kPlanMaskOff + MAX_SLOTS / 32 + 2 <= kPlanHdrInts, "validity bits fit the header");
+
+// Row sources of a unit: the routed ids in LDS (gate/up), or the unit's plan
+// record (down).  slots() gives lane r16 the slot of row r0 + r16 (the last
+// row past the count) and returns the expert's row count.
+struct RowsRoute {
+  const Route& rt;
+  template <int NT>
+  __device__ __forceinline__ int slots(const LayerArgs& a, int e, int r0, int (&sl)[NT]) const {
+    return lane_slots<NT>(a, rt, e, r0, sl);
+  }
+};
+struct RowsPlan {
+  int cnt;   // the expert's row count (wave-uniform)
+  int slot;  // this lane's slot, from the record (lanes r16 hold rows r0 + r16)
+  template <int NT>
+  __device__ __forceinline__ int slots(const LayerArgs&, int, int, int (&sl)[NT]) const {
+    static_assert(NT == 1, "a plan record holds one 16-row tile");
+    sl[0] = slot;
+    return cnt;
+  }
+};
+
 // Compile-time geometry of a (tier, phase, tiles-per-pass) instantiation.
 template <int TIER, int PH, int NT>
 struct Geo {
@@ -507,12 +545,13 @@ __device__ __forceinline__ void finish_pass(const LayerArgs& a, const UnitCtx<TI
 // arguments, so every load lands in a register of its own with no branch
 // between the loads and their use).
 template <bool BF, int ROWS_B, int NS, bool WF32>  // WF32: fp32 router weights (else 16-bit)
-__device__ __forceinline__ void combine_block_ns(const LayerArgs& a, const Route& rt, int blk) {
+__device__ __forceinline__ void combine_block_ns(const LayerArgs& a, int blk) {
   constexpr int SB = 8 / NS;  // slots per batch (eight slots: every k + shared of these configurations)
   constexpr bool wf32 = WF32;
   const int64_t set = (int64_t)a.T * a.kp * a.H;  // floats per partial set
   const __amdgpu_buffer_rsrc_t part_r = make_rsrc(a.part, a.nsplit * set * 4);
   const __amdgpu_buffer_rsrc_t w_r = make_rsrc(a.topk_w, (int64_t)a.T * a.k * (wf32 ? 4 : 2));
+  const uint32_t* valid = reinterpret_cast<const uint32_t*>(a.plan + kPlanMaskOff);
   const int h0 = blk * ROWS_B;
   for (int idx = threadIdx.x; idx < a.T * (ROWS_B / 4); idx += DNT) {
     const int t = idx / (ROWS_B / 4);
@@ -532,7 +571,8 @@ __device__ __forceinline__ void combine_block_ns(const LayerArgs& a, const Route
                           0, CPOL_SC1));
       // (the weights after the partial loads: converting them waits for
       // loads that are all in flight already)
-      // raw weights of the routed slots (zeros otherwise)
+      // raw weights of the routed slots (zeros otherwise), and the validity
+      // bits of slots t*k + j0 .. (a 64-bit window holds the batch's SB <= 8)
       uint32_t wr[SB];
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
@@ -543,12 +583,14 @@ __device__ __forceinline__ void combine_block_ns(const LayerArgs& a, const Route
         else
           wr[i] = __builtin_amdgcn_raw_buffer_load_b16(w_r, in ? q * 2 : OOB_OFF, 0, 0);
       }
+      const int b0 = t * a.k + j0;
+      const uint64_t vw = ((uint64_t)valid[(b0 >> 5) + 1] << 32 | valid[b0 >> 5]) >> (b0 & 31);
 #pragma unroll
       for (int i = 0; i < SB; ++i) {
         const int j = j0 + i;
         if (j < a.kp) {
-          // a dropped slot's partial rows were never written: zeros instead
-          const bool ok = j >= a.k || rt.ids[t * a.k + j] >= 0;
+          // a dropped slot (id outside [0, E)) never wrote its partial rows: zeros instead
+          const bool ok = j >= a.k || ((vw >> i) & 1u);
           const float wf = j >= a.k                    ? 1.f
                            : wf32                      ? __builtin_bit_cast(float, wr[i])
                            : a.w_dtype == EXQ_DTYPE_BF16 ? bf16_bits_to_f32(wr[i])
@@ -576,15 +618,15 @@ __device__ __forceinline__ void combine_block_ns(const LayerArgs& a, const Route
 }
 
 template <bool BF, int ROWS_B>
-__device__ __forceinline__ void combine_block(const LayerArgs& a, const Route& rt, int blk) {
+__device__ __forceinline__ void combine_block(const LayerArgs& a, int blk) {
   // in-kernel combines run with fewer than kCombineLaunchMinSplit splits
   const bool wf32 = a.w_dtype == EXQ_DTYPE_F32;
   if (a.nsplit == 1)
-    wf32 ? combine_block_ns<BF, ROWS_B, 1, true>(a, rt, blk) : combine_block_ns<BF, ROWS_B, 1, false>(a, rt, blk);
+    wf32 ? combine_block_ns<BF, ROWS_B, 1, true>(a, blk) : combine_block_ns<BF, ROWS_B, 1, false>(a, blk);
   else if (a.nsplit == 2)
-    wf32 ? combine_block_ns<BF, ROWS_B, 2, true>(a, rt, blk) : combine_block_ns<BF, ROWS_B, 2, false>(a, rt, blk);
+    wf32 ? combine_block_ns<BF, ROWS_B, 2, true>(a, blk) : combine_block_ns<BF, ROWS_B, 2, false>(a, blk);
   else
-    wf32 ? combine_block_ns<BF, ROWS_B, 3, true>(a, rt, blk) : combine_block_ns<BF, ROWS_B, 3, false>(a, rt, blk);
+    wf32 ? combine_block_ns<BF, ROWS_B, 3, true>(a, blk) : combine_block_ns<BF, ROWS_B, 3, false>(a, blk);
   __syncthreads();
   if (threadIdx.x == 0) {
     __hip_atomic_store(sync_c(a, blk), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -598,15 +640,15 @@ __device__ __forceinline__ void combine_block(const LayerArgs& a, const Route& r
 // block (n_tiles units times the k-splits write each block); the last of the
 // block's units combines the block.
 template <bool BF, int ROWS_B>
-__device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Route& rt, int blk,
-                                                    int n_tiles, int* s_flag) {
+__device__ __forceinline__ void publish_and_combine(const LayerArgs& a, int blk, int n_tiles,
+                                                    int* s_flag) {
   if (threadIdx.x == 0) {
     const int old =
         __hip_atomic_fetch_add(sync_c(a, blk), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *s_flag = old == n_tiles * a.nsplit - 1;
   }
   __syncthreads();
-  if (*s_flag) combine_block<BF, ROWS_B>(a, rt, blk);
+  if (*s_flag) combine_block<BF, ROWS_B>(a, blk);
 }
 
 // INT4 unit whose k-blocks fit the wave's LDS region (nmy <= CK): every
@@ -618,8 +660,8 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, const Ro
 // the weights in flight, so a work-group's whole slice is requested at once.
 // Activation fragments (and the fp16 group scales) stream through a 2-deep
 // register ring.
-template <bool BF, int PH, int NT>
-__device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt, int e, int blk,
+template <bool BF, int PH, int NT, typename Rows>
+__device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Rows& rows, int e, int blk,
                                              int sp, int tile, unsigned char* lds, int widx = -1) {
   using G = Geo<2, PH, NT>;
   constexpr int RS = G::RS, CK = G::CK;
@@ -662,7 +704,7 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
   // this unit's rows: tile `tile` of the expert's rows (one pass)
   const int r_begin = tile * NT * 16;
   int sl[NT];
-  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, r_begin, sl));
+  const int cnt = __builtin_amdgcn_readfirstlane(rows.template slots<NT>(a, e, r_begin, sl));
 
   const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
@@ -747,8 +789,8 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Route& rt
 // so those waits are fixed counts.  Separate arrays let the compiler see
 // that reading one k-block cannot touch another's pending copy.  The partial
 // tiles go to k-block 0's array once the loop is done.
-template <bool BF, int PH>
-__device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Route& rt, int e, int blk,
+template <bool BF, int PH, typename Rows>
+__device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Rows& rows, int e, int blk,
                                             int sp, int tile, bool prio) {
   constexpr int NT = 1;
   using G = Geo<2, PH, NT>;
@@ -795,7 +837,7 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Route& rt,
   copy_kb(0);
   const int r_begin = tile * 16;
   int sl[NT];
-  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, r_begin, sl));
+  const int cnt = __builtin_amdgcn_readfirstlane(rows.template slots<NT>(a, e, r_begin, sl));
   const int xo = u.xoff(a, sl[0]);
   uint4 areg[2][4];
   auto load_a = [&](int p, int kbl) {  // zeros past the wave's range
@@ -1002,8 +1044,8 @@ __device__ __forceinline__ void run_unit_dma_chunked(const LayerArgs& a, const R
 // (and contributes exactly zero), so the number of loads in flight is the
 // same on every path and each slot waits only for its own loads.  The first
 // ring fill of weights is issued before the expert's rows are gathered.
-template <int TIER, bool BF, int PH, int NT>
-__device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& rt, int e, int blk,
+template <int TIER, bool BF, int PH, int NT, typename Rows>
+__device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Rows& rows, int e, int blk,
                                               int sp, int tile, unsigned char* lds, int widx = -1) {
   using G = Geo<TIER, PH, NT>;
   constexpr int RS = G::RS, QPK = G::QPK, P = G::P;
@@ -1082,7 +1124,7 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
   // this unit's rows: tile `tile` of the expert's rows (one pass)
   const int r_begin = tile * NT * 16;
   int sl[NT];
-  const int cnt = __builtin_amdgcn_readfirstlane(lane_slots<NT>(a, rt, e, r_begin, sl));
+  const int cnt = __builtin_amdgcn_readfirstlane(rows.template slots<NT>(a, e, r_begin, sl));
 
   for (int r0 = r_begin; r0 < cnt && r0 < r_begin + NT * 16; r0 += NT * 16) {
     const int cc = cnt - r0 < NT * 16 ? cnt - r0 : NT * 16;
@@ -1200,50 +1242,106 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Route& r
   }
 }
 
-// A grid of at most one resident round of work-groups; each routes once and
-// then takes units blockIdx.x, blockIdx.x + gridDim.x, ... (expert-major:
-// unit u is row block u % nb of the (u / nb)-th active expert).
+// One unit of either phase: the tier (mixed banks) and the INT4 path pick its
+// routine.  `rt` is the work-group's routing (only the chunked gate/up path
+// reads it directly).
+template <bool BF, int PH, int NT, bool MIXED, int PATH, typename Rows>
+__device__ __forceinline__ void run_unit_any(const LayerArgs& a, const Rows& rows, const Route* rt,
+                                             int e, int blk, int sp, int t, uint32_t ev,
+                                             unsigned char* dyn_lds, bool prio) {
+  const int tier = (int)(ev >> 30);
+  const int widx = MIXED ? (int)(ev & kRowMask) : -1;
+  if (!MIXED || tier == 2) {
+    if constexpr (PATH == 1 && NT == 1 && !MIXED)
+      run_unit_kb<BF, PH>(a, rows, e, blk, sp, t, prio);
+    else if constexpr (PATH == 1)
+      run_unit_dma<BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx);
+    else if constexpr (PATH == 2 && PH == 0)
+      run_unit_dma_chunked<BF, NT>(a, *rt, e, blk, t, dyn_lds);
+    else
+      run_unit_ring<2, BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx);
+  } else if constexpr (MIXED) {
+    if (tier == 1)
+      run_unit_ring<1, BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx);
+    else
+      run_unit_ring<0, BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx);
+  }
+}
+
+// Gate/up (PH 0): a grid of at most one resident round of work-groups; each
+// routes once and then takes units blockIdx.x, blockIdx.x + gridDim.x, ...
+// (unit u is row block u % nb of the (u / nb)-th tile), and finally writes
+// its share of the down kernel's plan.  Down (PH 1): each unit's tile record
+// comes from that plan.
 // Four waves per SIMD (four work-groups per CU, at most 128 VGPRs), the
 // mixed-tier down kernel included: its BF16 and INT8 units hold their 64
 // weight rows in two passes of 32 (run_unit_ring), which keeps it within 128
 // registers without spills (at two waves per SIMD it left half the resident
 // slots empty: DeepSeek-V2-Lite T=64 120.5 -> 118.0 us, the mixed OLMoE
 // stack at T=32 88.9 -> 87.0).
-template <bool BF, int PH, int NT, bool MIXED, int PATH>  // INT4 path: 0 ring, 1 LDS, 2 chunked LDS
-__global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
+// The down kernel's plan (see kPlanHdrInts), written by wave 0 of the
+// gate/up work-groups from their routing: tile j's record by work-group
+// gridDim.x - 1 - (j % gridDim.x), the tile count and the validity bits by the
+// last work-group.
+template <bool MIXED>
+__device__ __forceinline__ void write_plan(const LayerArgs& a, const Route& rt, const uint32_t* cntw,
+                                        const int* emap, uint32_t word, int incl, int c,
+                                        int incl_u, int n_tiles, int nb) {
+  const int lane = threadIdx.x & 63;
+  const int w_last = (int)gridDim.x - 1 - (int)blockIdx.x;
+  for (int j = w_last; j < n_tiles; j += gridDim.x) {
+    const int u = j * nb;  // the tile's first unit
+    const int t = __popcll(__ballot(incl_u <= u));
+    const int v = u - (t > 0 ? __builtin_amdgcn_readlane(incl_u, t - 1) : 0);
+    const int ai = v / nb;
+    const int e = t == 0 ? select_expert(ai, word, incl, c) : select_tiled_expert(a, cntw, rt, t, ai);
+    int sl[1];
+    const int cnt = lane_slots<1>(a, rt, e, t * 16, sl);
+    int* rec = a.plan + kPlanHdrInts + j * kPlanRecInts;
+    if (lane < 16) rec[kPlanSlotOff + lane] = sl[0];
+    if (lane == 0) {
+      rec[0] = e | (t << 16);
+      rec[1] = cnt;
+      rec[2] = MIXED ? emap[e] : 0;
+    }
+  }
+  if (w_last == 0) {
+    // validity bits of the routed slots, for the down kernel's combine
+    const int n = a.T * a.k;
+    for (int s0 = 0; s0 < n; s0 += 64) {
+      const uint64_t m = __ballot(s0 + lane < n && rt.ids[s0 + lane] >= 0);
+      if (lane < 2) a.plan[kPlanMaskOff + (s0 >> 5) + lane] = (int)(uint32_t)(m >> (32 * lane));
+    }
+    if (lane == 0) a.plan[0] = n_tiles;
+  }
+}
+
+template <bool BF, int NT, bool MIXED, int PATH>
+__device__ __forceinline__ void decode_gateup(const LayerArgs& a, unsigned char* dyn_lds) {
+  constexpr int PH = 0;
   __shared__ Route rt;
-  __shared__ int s_flag;
   // rows per expert, behind the per-wave regions (the k-block LDS path keeps
   // its slices in static arrays and has only this in dynamic LDS)
   uint32_t* cntw =
       reinterpret_cast<uint32_t*>(dyn_lds + (PATH == 1 && NT == 1 && !MIXED ? 0 : DW * WAVE_LDS));
-  if constexpr (PH == 0) {
-    // the down launch that follows on this stream starts from zero counters,
-    // whatever an earlier call (or the caller's fill) left in the workspace
-    for (int i = blockIdx.x * DNT + threadIdx.x; i <= kDecodeMaxHBlocks; i += gridDim.x * DNT)
-      __hip_atomic_store(sync_c(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // the down launch that follows on this stream starts from zero counters,
+  // whatever an earlier call (or the caller's fill) left in the workspace
+  for (int i = blockIdx.x * DNT + threadIdx.x; i <= kDecodeMaxHBlocks; i += gridDim.x * DNT)
+    __hip_atomic_store(sync_c(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // mixed banks: every expert's (tier << 30) | row, behind the row counts
   int* emap = reinterpret_cast<int*>(cntw + ((a.Ep + 1) >> 1));
   uint32_t word;
   int incl, c;
   const int n_active = route<MIXED>(a, rt, cntw, word, incl, c, emap);
-  if (n_active == 0) {  // nothing routed: the output is zero
-    if (PH == 1) {
-      uint4* o = reinterpret_cast<uint4*>(a.out);
-      const int64_t n16 = (int64_t)a.T * a.H / 8;
-      for (int64_t i = (int64_t)blockIdx.x * DNT + threadIdx.x; i < n16;
-           i += (int64_t)gridDim.x * DNT)
-        o[i] = uint4{0u, 0u, 0u, 0u};
-    }
+  const int w_last = (int)gridDim.x - 1 - (int)blockIdx.x;  // 0 for the last work-group
+  if (n_active == 0) {  // nothing routed: the down kernel writes a zero output
+    if (w_last == 0 && threadIdx.x == 0) a.plan[0] = 0;
     return;
   }
-  // Unit u = (token tile, row block, k-split), the split fastest; tiles in
-  // segments (tile 0 of every active expert, then tile 1 of the experts with
-  // more than 16 rows, ...), so a busy expert's tiles run side by side.
-  const int ns = PH == 0 ? 1 : a.nsplit;
-  const int nb = (PH == 0 ? a.nbA : a.nbB) * ns;
+  // Unit u = (token tile, row block); tiles in segments (tile 0 of every
+  // active expert, then tile 1 of the experts with more than 16 rows, ...),
+  // so a busy expert's tiles run side by side.
+  const int nb = a.nbA;
   int n_tiles = n_active;
   int incl_u = n_active * nb;  // inclusive prefix of the segments' unit counts, lane t = segment t
   if (rt.multi) {              // (otherwise every expert is one tile: segment 0 only)
@@ -1257,40 +1355,79 @@ __global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
     }
   }
   const int n_units = n_tiles * nb;
-  // unit u -> (expert, row block, k-split, tile); uniform across the work-group
-  auto decode = [&](int u, int& e, int& blk, int& sp, int& t) {
+  // unit u -> (expert, row block, tile); uniform across the work-group
+  auto decode = [&](int u, int& e, int& blk, int& t) {
     t = __popcll(__ballot(incl_u <= u));  // segment = tile index
     const int v = u - (t > 0 ? __builtin_amdgcn_readlane(incl_u, t - 1) : 0);
     const int ai = v / nb;
-    const int bs = v - ai * nb;
-    blk = bs / ns;
-    sp = bs - blk * ns;
+    blk = v - ai * nb;
     e = t == 0 ? select_expert(ai, word, incl, c) : select_tiled_expert(a, cntw, rt, t, ai);
   };
+  const RowsRoute rows{rt};
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    int e, blk, sp, t;
-    decode(u, e, blk, sp, t);
+    int e, blk, t;
+    decode(u, e, blk, t);
     const uint32_t ev = MIXED ? (uint32_t)__builtin_amdgcn_readfirstlane(emap[e]) : (2u << 30);
-    const int tier = (int)(ev >> 30);
-    const int widx = MIXED ? (int)(ev & kRowMask) : -1;
-    if (!MIXED || tier == 2) {
-      if constexpr (PATH == 1 && NT == 1 && !MIXED)
-        run_unit_kb<BF, PH>(a, rt, e, blk, sp, t, n_units > 2 * (int)gridDim.x);
-      else if constexpr (PATH == 1)
-        run_unit_dma<BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
-      else if constexpr (PATH == 2 && PH == 0)
-        run_unit_dma_chunked<BF, NT>(a, rt, e, blk, t, dyn_lds);
-      else
-        run_unit_ring<2, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
-    } else if constexpr (MIXED) {
-      if (tier == 1)
-        run_unit_ring<1, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
-      else
-        run_unit_ring<0, BF, PH, NT>(a, rt, e, blk, sp, t, dyn_lds, widx);
-    }
-    if constexpr (PH == 1)
-      if (a.combine) publish_and_combine<BF, rows_b(NT)>(a, rt, blk, n_tiles, &s_flag);
+    run_unit_any<BF, PH, NT, MIXED, PATH>(a, rows, &rt, e, blk, 0, t, ev, dyn_lds,
+                                         n_units > 2 * (int)gridDim.x);
   }
+  // The down kernel's plan, after this work-group's own units (the last
+  // work-groups of the grid hold the fewest units); the routing state in LDS
+  // is untouched by the units (they use the per-wave regions and the k-block
+  // arrays).
+  if (threadIdx.x < 64) write_plan<MIXED>(a, rt, cntw, emap, word, incl, c, incl_u, n_tiles, nb);
+}
+
+template <bool BF, int NT, bool MIXED, int PATH>
+__device__ __forceinline__ void decode_down(const LayerArgs& a, unsigned char* dyn_lds) {
+  constexpr int PH = 1;
+  __shared__ int s_flag;
+  const int lane = threadIdx.x & 63;
+  const int ns = a.nsplit;
+  const int nb = a.nbB * ns;  // units per tile: row blocks x k-splits, the split fastest
+  // The first unit's record goes out beside the tile count (the grid has at
+  // most one work-group per unit of the largest plan, so the record index is
+  // inside the plan even before the count is known).
+  const int* recs = a.plan + kPlanHdrInts;
+  int u = blockIdx.x;
+  int j = u / nb;
+  int4 h = *reinterpret_cast<const int4*>(recs + j * kPlanRecInts);
+  int slot = recs[j * kPlanRecInts + kPlanSlotOff + (lane & 15)];
+  const int n_tiles = __builtin_amdgcn_readfirstlane(a.plan[0]);
+  if (n_tiles == 0) {  // nothing routed: the output is zero
+    uint4* o = reinterpret_cast<uint4*>(a.out);
+    const int64_t n16 = (int64_t)a.T * a.H / 8;
+    for (int64_t i = (int64_t)blockIdx.x * DNT + threadIdx.x; i < n16; i += (int64_t)gridDim.x * DNT)
+      o[i] = uint4{0u, 0u, 0u, 0u};
+    return;
+  }
+  const int n_units = n_tiles * nb;
+  while (u < n_units) {
+    const int bs = u - j * nb;
+    const int blk = bs / ns, sp = bs - blk * ns;
+    const int e = __builtin_amdgcn_readfirstlane(h.x & 0xffff);
+    const int t = __builtin_amdgcn_readfirstlane(h.x >> 16);
+    const RowsPlan rows{__builtin_amdgcn_readfirstlane(h.y), slot};
+    const uint32_t ev = MIXED ? (uint32_t)__builtin_amdgcn_readfirstlane(h.z) : (2u << 30);
+    run_unit_any<BF, PH, NT, MIXED, PATH>(a, rows, nullptr, e, blk, sp, t, ev, dyn_lds,
+                                         n_units > 2 * (int)gridDim.x);
+    if (a.combine) publish_and_combine<BF, rows_b(NT)>(a, blk, n_tiles, &s_flag);
+    u += gridDim.x;
+    if (u < n_units) {
+      j = u / nb;
+      h = *reinterpret_cast<const int4*>(recs + j * kPlanRecInts);
+      slot = recs[j * kPlanRecInts + kPlanSlotOff + (lane & 15)];
+    }
+  }
+}
+
+template <bool BF, int PH, int NT, bool MIXED, int PATH>  // INT4 path: 0 ring, 1 LDS, 2 chunked LDS
+__global__ void __launch_bounds__(DNT, 4) moe_decode_kernel(LayerArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char dyn_lds[];
+  if constexpr (PH == 0)
+    decode_gateup<BF, NT, MIXED, PATH>(a, dyn_lds);
+  else
+    decode_down<BF, NT, MIXED, PATH>(a, dyn_lds);
 }
 
 // The down phase's combine as a launch of its own (LayerArgs::combine == 0):
@@ -1807,6 +1944,13 @@ int resident_work_groups(const void* kern, int threads, size_t lds, int* out) {
   return EXQ_SUCCESS;
 }
 
+size_t decode_plan_bytes(int64_t T, int64_t k, int64_t E, int64_t n_shared) {
+  // tiles: one per active expert, plus one per further 16 rows of any expert
+  const int64_t active = (T * k < E ? T * k : E) + n_shared;
+  const int64_t tiles = active + (T * (k + n_shared) + 15) / 16;
+  return (size_t)(kPlanHdrInts + tiles * kPlanRecInts) * 4;
+}
+
 bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, int64_t H,
                            int64_t I, int64_t group_size) {
   const int64_t gkb = group_size / 128;  // k-blocks per scale group: a power of two
@@ -1845,6 +1989,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   a.part = d.part;
   a.out = d.out;
   a.sync = d.sync;
+  a.plan = d.plan;
   const bool mixed = d.tier != nullptr;
   const int nt = 1;
   a.nbA = d.I / 16;

@@ -152,8 +152,14 @@ struct DecodeLaunch {
   float* part;             // [kDecodeMaxSplit][T * kp, H]
   uint16_t* out;           // [T, H]
   int* sync;
+  int* plan;               // the down kernel's per-tile records (decode_plan_bytes)
   bool bf;
 };
+
+// Bytes of the decode plan: a 128-byte header line, then one 128-byte record
+// per 16-row tile (at most one per active expert plus one per further 16
+// routed rows).
+size_t decode_plan_bytes(int64_t T, int64_t k, int64_t E, int64_t n_shared);
 
 bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, int64_t H,
                            int64_t I, int64_t group_size);

@@ -461,7 +461,7 @@ namespace {
 
 // ---- workspace layout of the fused forward --------------------------------------
 struct FusedLayout {
-  size_t sync, hdr, ends, sorted, tg, mid, partial, rs, blk, total;
+  size_t sync, hdr, ends, sorted, tg, mid, partial, rs, blk, plan, total;
   int64_t n, tg_cap;
 };
 
@@ -491,6 +491,9 @@ FusedLayout fused_layout(const exq_moe_problem& p) {
   const int64_t rs_mid = tile_rowsum_floats(L.n, p.inter_size);
   L.rs = off;       off = align_up(off + (size_t)(rs_x > rs_mid ? rs_x : rs_mid) * 4, 256);
   L.blk = off;      off = align_up(off + (size_t)route_plan_blocks(L.n) * Ep * 4, 256);
+  L.plan = off;     off = align_up(off + (dec ? decode_plan_bytes(p.n_tokens, p.top_k,
+                                                                    p.n_experts, p.n_shared)
+                                              : 0), 256);
   L.total = off;
   return L;
 }
@@ -623,6 +626,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     d.part = reinterpret_cast<float*>(ws + L.partial);
     d.out = reinterpret_cast<uint16_t*>(out);
     d.sync = reinterpret_cast<int*>(ws + L.sync);
+    d.plan = reinterpret_cast<int*>(ws + L.plan);
     d.bf = bf;
     return launch_decode_layer(d, s);  // times its two kernels with the stage events
   } else if (general) {
