@@ -72,9 +72,13 @@ def parse_args():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other BASELINE.json configurations")
     ap.add_argument("--pmc-run", action="store_true",
-                    help="calibration copy + one eager pass, for rocprofv3 --pmc")
+                    help="calibration copy + eager passes over the layers, for rocprofv3")
+    ap.add_argument("--passes", type=int, default=1,
+                    help="with --pmc-run: eager passes over the layers (default 1)")
     ap.add_argument("--pmc-summary", type=str, default="",
                     help="per-kernel mean of a rocprofv3 counter CSV")
+    ap.add_argument("--north-star-only", action="store_true",
+                    help="measure only the OLMoE T=16 line (BASELINE configs[0]) and exit")
     ap.add_argument("--routing-only", action="store_true",
                     help="time only the standalone stable sort (exq_dispatch) and exit")
     ap.add_argument("--prefill-only", action="store_true",
@@ -351,7 +355,7 @@ class _Calls:
         self.x, self.ids, self.wts, self.out, self.ws = x, ids, wts, out, ws
 
 
-def measure_configs(dev, reps, cpu=None):
+def measure_configs(dev, reps, cpu=None, north_star_only=False):
     """The other BASELINE.json configurations: decode µs/layer and achieved GB/s
     on activated-expert bytes (weights + scales; shared experts included) over
     distinct seeded layers replayed from a HIP graph, and prefill TFLOP/s.
@@ -359,7 +363,8 @@ def measure_configs(dev, reps, cpu=None):
     Returns (rows, north_star, cpu_rows): north_star is the OLMoE T=16 line
     (the target configuration) with its own stage
     events and roofline; cpu_rows (when ``cpu`` holds the CPU settings) the
-    reference CPU path timed on layer 0 of each configuration, same inputs."""
+    reference CPU path timed on layer 0 of each configuration, same inputs.
+    ``north_star_only`` measures the OLMoE T=16 line alone (for profiling)."""
     import json as _json
     import tempfile
     import numpy as np
@@ -426,13 +431,14 @@ def measure_configs(dev, reps, cpu=None):
                                       tid.reshape(-1).tolist())
             cpu_rows.append(cpu_config_row(name, T, x, routed, shared, tid, tw, cpu))
 
-    # OLMoE single INT4 layer; 3 distinct layers so the 198 MiB
-    # bank does not sit in the 256 MB Infinity Cache between calls
+    # OLMoE single INT4 layer; 48 distinct seeded layers (9.3 GiB)
+    # rotated, so no bank sits in the 256 MB Infinity Cache between its calls
+    # (the same layers as the counter runs of profiles/)
     cfg = synth.CONFIGS["olmoe"]
-    layers = int4_layers(cfg, 3)
+    layers = int4_layers(cfg, 48)
     eb = synth.int4_expert_bytes(cfg.hidden, cfg.inter, cfg.group_size)
     w13_bytes = 2 * cfg.inter * cfg.hidden // 2 + 2 * cfg.inter * (cfg.hidden // cfg.group_size) * 2
-    for T in (1, 16, 64):
+    for T in ((16,) if north_star_only else (1, 16, 64)):
         x = torch.from_numpy(synth.hidden_np(T, cfg.hidden, 77 + T)).to(torch.bfloat16).to(dev)
         ws = ws_for(cfg, T)
         calls, nbytes, active, rts = [], 0, [], []
@@ -464,6 +470,8 @@ def measure_configs(dev, reps, cpu=None):
         cpu_int4("olmoe", T, x, layers[0], rts[0][0], rts[0][1])
     del layers
     torch.cuda.empty_cache()
+    if north_star_only:
+        return rows, north_star, cpu_rows
 
     # Mixed-precision OLMoE stack: 16 layers, BF16/INT8/INT4 per
     # expert from the quant-plan artifact (tiers ranked by the router's own
@@ -621,9 +629,37 @@ def stream_read_ceiling(dev, nbytes=2 << 30, reps=10):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
+    cross = stream_cross_check(buf, reps)
     del buf, sink
     return {"GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes, "reps": reps,
-            "kernel": "exq_stream_read (16-byte loads, 8 in flight per thread)"}
+            "kernel": "exq_stream_read (16-byte loads, 8 in flight per thread)",
+            "cross_check": cross}
+
+
+def stream_cross_check(buf, reps):
+    """Two other readers of the same buffer, timed the same way: torch's own
+    reduction kernel (a float32 sum over the bytes, which reads every byte once
+    and writes one value) and a device-to-device copy (torch's copy kernel; its
+    rate counts the bytes read, with as many written beside them)."""
+    import torch
+    out = {}
+    v = buf.view(torch.float32)
+    v.sum()
+    dst = torch.empty_like(buf)
+    dst.copy_(buf)
+    torch.cuda.synchronize()
+    for name, fn in (("torch_sum_read_GBps", lambda: v.sum()),
+                     ("d2d_copy_read_GBps", lambda: dst.copy_(buf))):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(buf.numel() / (e0.elapsed_time(e1) / reps * 1e-3) / 1e9, 1)
+    del dst
+    return out
 
 
 def stream_read_at_size(dev, nbytes, n_bufs=48, reps=5, grid=2048):
@@ -764,6 +800,10 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda", 0)
     cfg = synth.CONFIGS["qwen3" if not args.pmc_run else args.config]
+    if args.north_star_only:  # the OLMoE T=16 line alone (profiles)
+        _, ns, _ = measure_configs(dev, max(20, args.steps), None, north_star_only=True)
+        print(json.dumps({"north_star": ns}), flush=True)
+        return
     if args.routing_only:  # the standalone sort alone (profiles)
         print(json.dumps({"routing": routing_rows(dev, max(5, args.steps // 5))}), flush=True)
         return
@@ -797,10 +837,11 @@ def main():
 
     b = Batch(stack, args.batch, dev)
     if args.pmc_run:
-        run_step(stack, b)
+        for _ in range(max(1, args.passes)):
+            run_step(stack, b)
         torch.cuda.synchronize()
-        log(f"one eager pass of {args.layers} layers at T={args.batch}; activated experts "
-            f"per layer {sum(b.active) / len(b.active):.2f}")
+        log(f"{max(1, args.passes)} eager pass(es) of {args.layers} layers at T={args.batch}; "
+            f"activated experts per layer {sum(b.active) / len(b.active):.2f}")
         return
     ms, wall, per = time_steps(stack, b, args.steps, args.warmup, use_graph)
     per_layer = [m * 1e3 / args.layers for m in per]  # µs/layer of each step
