@@ -7,8 +7,8 @@
 namespace exq {
 
 // Tokens of one expert are processed in groups of at most this many rows:
-// four 16-row MFMA tiles on the grouped kernel, eight on the tiled prefill
-// kernels (128-row tiles).
+// four 16-row MFMA tiles on the grouped kernel and on the 64 x 256 INT4 tiles
+// of the prefill kernels, eight on the 128 x 128 tiles.
 constexpr int kTokenGroup = 64;
 constexpr int kTokenGroupI4 = 128;
 
@@ -70,11 +70,15 @@ struct GemmArgs {
 // scaled by the nibble base, from launch_group_rowsum (rs [K / 128][rs_rows];
 // GATEUP rows are tokens, DOWN / PLAIN rows are expert-sorted positions).
 bool tile_gemm_applies(int tier, int mode, int n_rows, int inter, int K, int group_size);
+// The INT4 tiles can be 64 expert-sorted rows x 256 weight rows instead (token
+// groups of kTokenGroup rows): GATEUP needs I % 128 == 0, DOWN / PLAIN rows % 256.
+bool tile_gemm_wide_applies(int mode, int n_rows, int inter);
 int64_t tile_rowsum_floats(int64_t rows, int64_t K);
 int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows, int K, int gs,
                         float* out, hipStream_t s);
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
-                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s);
+                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s,
+                     bool wide = false);
 
 // INT4 grouped GEMMs for the shapes outside the tiled / grouped kernels
 // (general.hip): K % 32 == 0, a group size that is a multiple of 32 dividing

@@ -561,8 +561,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   rp.sorted = reinterpret_cast<int*>(ws + L.sorted);
   rp.tg = reinterpret_cast<TgEntry*>(ws + L.tg);
   rp.tg_cap = (int)L.tg_cap;
-  // INT4 and BF16 experts run on the tiled kernels (128-row token groups)
-  // when both projections fit them and the gathered activations are 32-bit
+  // INT4 and BF16 experts run on the tiled kernels (128- or 64-row token
+  // groups) when both projections fit them and the gathered activations are 32-bit
   // addressable; INT8 experts (and everything else) on the grouped kernel.
   const int gs = (int)p->group_size;
   // all-INT4 layers of other shapes: routing plan + general kernels + combine
@@ -577,7 +577,17 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   const bool tile_bf = tier != nullptr && x32 &&
                        tile_gemm_applies(0, MODE_GATEUP, 2 * I, I, H, gs) &&
                        tile_gemm_applies(0, MODE_DOWN, H, I, I, gs);
-  rp.i4_group = tile ? kTokenGroupI4 : kTokenGroup;
+  // INT4 tiles of 64 sorted rows x 256 weight rows when both projections take
+  // them and the routed experts average fewer than 512 rows: the same MFMA
+  // work per chunk from fewer bytes of copies, and about half the padding rows
+  // of 128-row groups (DeepSeek-V2-Lite at 2048 tokens, 192 rows per expert:
+  // 627 -> 585 us).  With more rows per expert there is little padding to save
+  // and the 128 x 128 tile's 8 MFMAs per dequantised weight fragment win
+  // (Mixtral at 4096 tokens, 1024 rows per expert: 3518 -> 3612 us wide).
+  const bool wide = tile && tile_gemm_wide_applies(MODE_GATEUP, 2 * I, I) &&
+                    tile_gemm_wide_applies(MODE_DOWN, H, I) &&
+                    (int64_t)T * k < 512 * (int64_t)E;
+  rp.i4_group = tile ? (wide ? kTokenGroup : kTokenGroupI4) : kTokenGroup;
   rp.bf_group = tile_bf ? kTokenGroupI4 : kTokenGroup;
   rp.counters = nullptr;
   rp.n_counters = 0;
@@ -702,7 +712,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     if (run_tile) {
       st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
       if (st) return st;
-      st = launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s);
+      st = launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s, wide);
       if (st) return st;
     }
     st = record_stage(2, s);
@@ -728,7 +738,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
     if (run_tile) {
       st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
       if (st) return st;
-      st = launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s);
+      st = launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s, wide);
       if (st) return st;
     }
   }

@@ -37,10 +37,7 @@ namespace exq {
 namespace {
 
 constexpr int TT = 256;              // threads per work-group (4 waves)
-constexpr int TM = 128;              // expert-sorted rows per tile
 constexpr int KC = 128;              // contraction per chunk
-constexpr int A_STAGE = TM * KC * 2; // 32 KiB of activations per chunk
-constexpr int B_STAGE = 128 * KC / 2;  // 8 KiB of packed weights per chunk
 
 typedef void __attribute__((address_space(3)))* lptr_t;
 
@@ -152,7 +149,7 @@ struct TileArgs {
   const float* rs;   // INT4: [K / 128][rs_rows] base * (row sum over the group)
   int rs_rows;
   int64_t x_bytes;   // bytes addressable from a.x (GATEUP gather)
-  int n_tiles;       // weight tiles per expert (I / 64 for GATEUP, rows / 128 otherwise)
+  int n_tiles;       // weight tiles per expert (I / (TN / 2) for GATEUP, rows / TN otherwise)
 };
 
 // ---- shared pieces of the tiled kernels --------------------------------------
@@ -178,23 +175,26 @@ __device__ __forceinline__ bool tile_unit(const GemmArgs& a, int t0, int n, int 
   return true;
 }
 
-// Weight row (within the expert) of LDS weight row rho of tile nt.
-template <int MODE>
+// Weight row (within the expert) of LDS weight row rho of tile nt, for a
+// tile of TN weight rows (GATEUP: TN / 2 gate rows j0.. and the matching up rows).
+template <int MODE, int TN = 128>
 __device__ __forceinline__ int tile_wrow(const GemmArgs& a, int nt, int rho) {
+  constexpr int HN = TN / 2;
   if constexpr (MODE == MODE_GATEUP)
-    return rho < 64 ? nt * 64 + rho : a.inter + nt * 64 + (rho - 64);
+    return rho < HN ? nt * HN + rho : a.inter + nt * HN + (rho - HN);
   else
-    return nt * 128 + rho;
+    return nt * TN + rho;
 }
 
-// First LDS weight row of n-tile t of wave column wn (NTW tiles per wave).
-// GATEUP: the first half of a wave's tiles are gate rows, the second half the
-// up rows of the same j.
-template <int MODE, int NTW>
+// First LDS weight row of n-tile t of wave column wn (NTW tiles per wave) in
+// a tile of TN weight rows.  GATEUP: the first half of a wave's tiles are gate
+// rows, the second half the up rows of the same j.
+template <int MODE, int NTW, int TN = 128>
 __device__ __forceinline__ int tile_brow(int wn, int t) {
   constexpr int HALF = NTW / 2;
+  constexpr int HN = TN / 2;  // gate rows of the tile
   if constexpr (MODE == MODE_GATEUP)
-    return t < HALF ? wn * HALF * 16 + t * 16 : 64 + wn * HALF * 16 + (t - HALF) * 16;
+    return t < HALF ? wn * HALF * 16 + t * 16 : HN + wn * HALF * 16 + (t - HALF) * 16;
   else
     return wn * NTW * 16 + t * 16;
 }
@@ -210,8 +210,9 @@ __device__ __forceinline__ int tile_xrow(const GemmArgs& a, const TgEntry& te, i
     return te.pos0 + mm;
 }
 
-// Store a wave's finished sub-tile (rows wm*MT*16.., MFMA output layout).
-template <bool BF, int MODE, int MT, int NTW>
+// Store a wave's finished sub-tile (rows wm*MT*16.., MFMA output layout) of a
+// tile TN weight rows wide.
+template <bool BF, int MODE, int MT, int NTW, int TN = 128>
 __device__ __forceinline__ void tile_store(const GemmArgs& a, const TgEntry& te, int nt, int wm,
                                            int wn, int r16, int kq,
                                            const f32x4_t (&tot)[MT][NTW]) {
@@ -225,18 +226,18 @@ __device__ __forceinline__ void tile_store(const GemmArgs& a, const TgEntry& te,
       const int pos = te.pos0 + m;
       if constexpr (MODE == MODE_GATEUP) {
         uint16_t* mid = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
-                        nt * 64 + wn * HALF * 16 + r16;
+                        nt * (TN / 2) + wn * HALF * 16 + r16;
 #pragma unroll
         for (int t = 0; t < HALF; ++t)
           mid[t * 16] = (uint16_t)to_act_bits<BF>(silu_f32(tot[mt][t][v_]) * tot[mt][t + HALF][v_]);
       } else if constexpr (MODE == MODE_PLAIN) {
         uint16_t* c = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
-                      nt * 128 + wn * NTW * 16 + r16;
+                      nt * TN + wn * NTW * 16 + r16;
 #pragma unroll
         for (int t = 0; t < NTW; ++t) c[t * 16] = (uint16_t)to_act_bits<BF>(tot[mt][t][v_]);
       } else {
         const int slot = a.row_slot[pos];
-        float* part = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.out_stride + nt * 128 +
+        float* part = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.out_stride + nt * TN +
                       wn * NTW * 16 + r16;
 #pragma unroll
         for (int t = 0; t < NTW; ++t) part[t * 16] = tot[mt][t][v_];
@@ -245,13 +246,21 @@ __device__ __forceinline__ void tile_store(const GemmArgs& a, const TgEntry& te,
   }
 }
 
-// MT = m-tiles (16 rows) per wave: 4 -> waves 2 x 2 of 64 x 64; 8 -> 1 x 4 of 128 x 32.
-template <bool BF, int MODE, int MT>
+// The four waves are one row of the tile (1 x 4): each wave holds all TM =
+// 16 MT token rows and NTW 16-row weight tiles, so TN = 64 NTW.
+//   MT = 8, NTW = 2: 128 x 128 (each dequantised weight fragment feeds 8 MFMAs);
+//   MT = 4, NTW = 4:  64 x 256 (the same MFMA work per chunk from 16 + 16 KiB of
+//                     copies instead of 32 + 8 KiB: activation chunks, re-read
+//                     from L2 for every weight tile, are the larger stream).
+template <bool BF, int MODE, int MT, int NTW>
 __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs ta) {
-  constexpr int WAVES_M = 8 / MT;
-  constexpr int WAVES_N = 4 / WAVES_M;
-  constexpr int NTW = 8 / WAVES_N;  // n-tiles (16 weight rows) per wave
-  constexpr int RSR = MT / 4;       // row sums held per lane (64 rows each)
+  constexpr int WAVES_N = 4;
+  constexpr int TM = MT * 16, TN = NTW * 16 * WAVES_N;
+  constexpr int A_STAGE = TM * KC * 2;  // activations per chunk
+  constexpr int B_STAGE = TN * KC / 2;  // packed weights per chunk
+  constexpr int QA = TM / 16;           // activation copies per wave and chunk (4 rows each)
+  constexpr int QB = TN / 64;           // weight copies per wave and chunk (16 rows each)
+  constexpr int RSR = MT / 4;           // row sums held per lane (64 rows each)
   __shared__ __attribute__((aligned(1024))) unsigned char sA0[A_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sA1[A_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sB0[B_STAGE];
@@ -265,7 +274,7 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS DMA bases in SGPRs
   const int r16 = lane & 15, kq = lane >> 4;
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int wm = 0, wn = wave;
   const int K = a.K;
   const int nch = K / KC;
   const int ngs = K / KC;  // scale groups (group_size == KC)
@@ -273,8 +282,8 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   const int widx = a.w.index ? a.w.index[te.e] : te.e;
   const int64_t ebase = (int64_t)widx * a.n_rows;
   const int rowbytes = K / 2;
-  auto wrow = [&](int rho) { return tile_wrow<MODE>(a, nt, rho); };
-  auto brow = [&](int t) { return tile_brow<MODE, NTW>(wn, t); };
+  auto wrow = [&](int rho) { return tile_wrow<MODE, TN>(a, nt, rho); };
+  auto brow = [&](int t) { return tile_brow<MODE, NTW, TN>(wn, t); };
   auto x_row = [&](int m) { return tile_xrow<MODE>(a, te, m); };
 
   const __amdgpu_buffer_rsrc_t wr =
@@ -292,17 +301,17 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   const __amdgpu_buffer_rsrc_t rnull = make_rsrc(ta.rs, 0);
 
   // ---- per-lane DMA offsets ------------------------------------------------
-  int voffA[8], voffB[2];
+  int voffA[QA], voffB[QB];
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {  // LDS rows 4j..4j+3 per instruction, 16 columns each
-    const int m = (wave * 8 + q) * 4 + (lane >> 4);
+  for (int q = 0; q < QA; ++q) {  // LDS rows 4j..4j+3 per instruction, 16 columns each
+    const int m = (wave * QA + q) * 4 + (lane >> 4);
     const int c = (lane & 15) ^ a_swz(m & 15);
     const int xrow = x_row(m);
     voffA[q] = (MODE == MODE_GATEUP ? xrow : xrow - pos0) * (int)a.x_stride * 2 + c * 16;
   }
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {  // LDS rows 16j..16j+15 per instruction, 4 columns each
-    const int rho = (wave * 2 + q) * 16 + (lane >> 2);
+  for (int q = 0; q < QB; ++q) {  // LDS rows 16j..16j+15 per instruction, 4 columns each
+    const int rho = (wave * QB + q) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ b_swz(rho & 15);
     voffB[q] = wrow(rho) * rowbytes + c * 16;
   }
@@ -334,9 +343,9 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
     unsigned char* A = st ? sA1 : sA0;
     unsigned char* B = st ? sB1 : sB0;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) dma16(ok ? xr : xnull, A + (wave * 8 + q) * 1024, voffA[q], chl * 256);
+    for (int q = 0; q < QA; ++q) dma16(ok ? xr : xnull, A + (wave * QA + q) * 1024, voffA[q], chl * 256);
 #pragma unroll
-    for (int q = 0; q < 2; ++q) dma16(ok ? wr : wnull, B + (wave * 2 + q) * 1024, voffB[q], chl * 64);
+    for (int q = 0; q < QB; ++q) dma16(ok ? wr : wnull, B + (wave * QB + q) * 1024, voffB[q], chl * 64);
 #pragma unroll
     for (int t = 0; t < NTW; ++t)
       sc_raw[st][t] =
@@ -411,7 +420,7 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
 #undef EXQ_TILE_CHUNK
   wait_vm_all();  // the last (empty) prefetch has drained before the work-group ends
 
-  tile_store<BF, MODE, MT, NTW>(a, te, nt, wm, wn, r16, kq, tot);
+  tile_store<BF, MODE, MT, NTW, TN>(a, te, nt, wm, wn, r16, kq, tot);
 }
 
 // ---- BF16 experts ------------------------------------------------------------
@@ -596,7 +605,7 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
 }
 
 template <int MODE>
-static int launch_tile_mode(int tier, bool bf, const GemmArgs& a, const TileArgs& t,
+static int launch_tile_mode(int tier, bool bf, bool wide, const GemmArgs& a, const TileArgs& t,
                             int64_t grid, hipStream_t s) {
   const dim3 g((unsigned)grid), b(TT);
   if (tier == 0) {
@@ -606,27 +615,41 @@ static int launch_tile_mode(int tier, bool bf, const GemmArgs& a, const TileArgs
       hipLaunchKernelGGL((tile_gemm_bf16_kernel<false, MODE>), g, b, 0, s, a, t);
     return check_launch("tile_gemm_bf16_kernel");
   }
+  if (wide) {
+    if (bf)
+      hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 4, 4>), g, b, 0, s, a, t);
+    else
+      hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 4, 4>), g, b, 0, s, a, t);
+    return check_launch("tile_gemm_kernel");
+  }
   if (bf)
-    hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 8>), g, b, 0, s, a, t);
+    hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 8, 2>), g, b, 0, s, a, t);
   else
-    hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 8>), g, b, 0, s, a, t);
+    hipLaunchKernelGGL((tile_gemm_kernel<false, MODE, 8, 2>), g, b, 0, s, a, t);
   return check_launch("tile_gemm_kernel");
 }
 
+bool tile_gemm_wide_applies(int mode, int n_rows, int inter) {
+  return mode == MODE_GATEUP ? inter % 128 == 0 : n_rows % 256 == 0;
+}
+
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
-                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s) {
+                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s,
+                     bool wide) {
   TileArgs t;
   t.rs = rs;
   t.rs_rows = (int)rs_rows;
   t.x_bytes = x_bytes;
-  t.n_tiles = mode == MODE_GATEUP ? a.inter / 64 : a.n_rows / 128;
+  wide = wide && tier == 2;
+  const int tn = wide ? 256 : 128;
+  t.n_tiles = mode == MODE_GATEUP ? a.inter / (tn / 2) : a.n_rows / tn;
   const int64_t grid = 8 * cdiv(tg_cap, 8) * t.n_tiles;
   if (grid <= 0) return EXQ_SUCCESS;
   if (grid > INT32_MAX || rs_rows > INT32_MAX)
     return set_error(EXQ_ERROR_UNSUPPORTED, "tile_gemm: problem too large");
-  if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(tier, bf, a, t, grid, s);
-  if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(tier, bf, a, t, grid, s);
-  return launch_tile_mode<MODE_PLAIN>(tier, bf, a, t, grid, s);
+  if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(tier, bf, wide, a, t, grid, s);
+  if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(tier, bf, wide, a, t, grid, s);
+  return launch_tile_mode<MODE_PLAIN>(tier, bf, wide, a, t, grid, s);
 }
 
 }  // namespace exq

@@ -18,6 +18,10 @@ pytestmark = pytest.mark.gpu
 TOL = 5e-3
 
 WIDE = synth.MoeConfig("prefill_wide", 41, 1024, 512, 8, 2, True)
+# two experts, both on every token: far more than 512 rows per expert, so the
+# INT4 tiles are 128 rows x 128 weight rows (fewer rows per expert take the
+# 64 x 256 tiles, as WIDE does)
+FEW = synth.MoeConfig("prefill_few", 47, 1024, 512, 2, 2, True, zipf=False)
 
 
 def _pack(E, I, H, seed, device, group_size=128):
@@ -32,12 +36,12 @@ def _hidden(T, H, seed, device, dtype):
     return torch.from_numpy(synth.hidden_np(T, H, seed)).to(dtype).to(device)
 
 
-@pytest.mark.parametrize("T,dtype", [(300, torch.bfloat16), (300, torch.float16),
-                                     (1100, torch.bfloat16)])
-def test_prefill_fused_zipf_routing(T, dtype, device):
+@pytest.mark.parametrize("cfg,T,dtype", [(WIDE, 300, torch.bfloat16), (WIDE, 300, torch.float16),
+                                         (WIDE, 1100, torch.bfloat16), (FEW, 1100, torch.bfloat16),
+                                         (FEW, 1100, torch.float16)])
+def test_prefill_fused_zipf_routing(cfg, T, dtype, device):
     from exq_amd.kernels import fused_experts
-    cfg = WIDE
-    banner(f"prefill fused T={T} {dtype}")
+    banner(f"prefill fused {cfg.name} T={T} {dtype}")
     p13, s13, p2, s2 = _pack(cfg.n_experts, cfg.inter, cfg.hidden, 900, device)
     ids, w = synth.routing(cfg, T)
     counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
@@ -53,11 +57,12 @@ def test_prefill_fused_zipf_routing(T, dtype, device):
     assert np.array_equal(so.cpu().numpy(), r_so)
     assert np.array_equal(ends.cpu().numpy(), r_ends)
     ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
-    assert_close_rel(out, ref, TOL, f"prefill fused T={T} {dtype}")
+    assert_close_rel(out, ref, TOL, f"prefill fused {cfg.name} T={T} {dtype}")
 
 
 def test_prefill_one_expert_takes_all_rows(device):
-    """Every row on one expert: 600 rows = four full 128-row groups + 88."""
+    """Every row on one expert: 600 rows = nine full 64-row groups + 24 (and,
+    at 128 rows per group, four + 88)."""
     from exq_amd.kernels import fused_experts
     cfg = WIDE
     banner("prefill one expert")
