@@ -225,8 +225,27 @@ struct WideLds {
   uint32_t masks[MASK_WORDS];
 };
 
-// tot[] and run[] of block range [lo, ...) over all n items; keys are loaded
-// eight per thread before their LDS atomics, so the loads are in flight together.
+// hist[key(i)] += 1 for i in [a, z): keys are loaded eight per thread before
+// their LDS atomics, so the loads are in flight together.
+template <typename KeyFn>
+__device__ __forceinline__ void count_range(int a, int z, KeyFn key, int* hist) {
+  constexpr int U = 8;
+  for (int64_t i0 = a; i0 < z; i0 += RT * U) {
+    int kv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * RT + (int)threadIdx.x;
+      kv[u] = i < z ? key((int)i) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (kv[u] >= 0) atomicAdd(&hist[kv[u]], 1);
+  }
+}
+
+// tot[] (all n items) and before[] (the items before lo) per bucket; each
+// item costs one LDS atomic (the items from lo on count into tot, which then
+// adds before).
 template <typename KeyFn>
 __device__ void wide_count(int n, int lo, int nb, KeyFn key, int* tot, int* before) {
   for (int b = threadIdx.x; b < nb; b += RT) {
@@ -234,23 +253,10 @@ __device__ void wide_count(int n, int lo, int nb, KeyFn key, int* tot, int* befo
     before[b] = 0;
   }
   __syncthreads();
-  constexpr int U = 8;
-  for (int64_t i0 = 0; i0 < n; i0 += RT * U) {
-    int kv[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + u * RT + (int)threadIdx.x;
-      kv[u] = i < n ? key((int)i) : -1;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + u * RT + (int)threadIdx.x;
-      if (kv[u] >= 0) {
-        atomicAdd(&tot[kv[u]], 1);
-        if (i < lo) atomicAdd(&before[kv[u]], 1);
-      }
-    }
-  }
+  count_range(0, lo < n ? lo : n, key, before);
+  count_range(lo, n, key, tot);
+  __syncthreads();
+  for (int b = threadIdx.x; b < nb; b += RT) tot[b] += before[b];
   __syncthreads();
 }
 
@@ -417,8 +423,17 @@ __host__ __forceinline__ void wide_grid(int64_t n, int* grid, int* per) {
 // Bucket of slot t*kp + j: routed id (dropped: -1) for j < k, shared expert
 // E + (j - k) otherwise.
 __device__ __forceinline__ int plan_key(const RoutePlanParams& p, int slot) {
-  const int t = slot / p.kp;
-  const int j = slot - t * p.kp;
+  // slot / kp from a float reciprocal and one correction step: slot < 2^24
+  // (validated), so the estimate is off by at most one
+  int t = (int)((float)slot * (1.0f / (float)p.kp));
+  int j = slot - t * p.kp;
+  if (j >= p.kp) {
+    ++t;
+    j -= p.kp;
+  } else if (j < 0) {
+    --t;
+    j += p.kp;
+  }
   if (j < p.k) {
     int64_t v = load_index(p.ids, p.ids_dtype, (int64_t)t * p.k + j);
     return (v >= 0 && v < p.E) ? (int)v : -1;
@@ -503,7 +518,40 @@ __global__ void __launch_bounds__(RT) route_plan_kernel(RoutePlanParams p) {
   plan_tail(p, s);
 }
 
-// Large batches: the same plan over RB-slot blocks in three launches --
+// Large batches up to kRecountMaxSlots: the same plan in one launch with no
+// scratch, as the standalone sort does it -- every block counts all n slots'
+// buckets (split into the slots before its range and all), scans, and stably
+// scatters its own range; one more block (the last) only counts and runs the
+// tail from the totals, off the scatter blocks' path.
+constexpr int kRecountMaxSlots = 65536;
+
+__global__ void __launch_bounds__(RT) route_plan_recount_kernel(RoutePlanParams p, int per) {
+  __shared__ RouteLds s;
+  auto key = [&](int slot) { return plan_key(p, slot); };
+  const int nb = p.Ep;
+  const bool tail = blockIdx.x == gridDim.x - 1;
+  const int lo = tail ? p.n : blockIdx.x * per, hi = min(p.n, lo + per);
+  wide_count(p.n, lo, nb, key, s.cnt, s.run);
+  const int b = threadIdx.x;
+  int t;
+  const int ex = block_excl_scan(b < nb ? s.cnt[b] : 0, s.wsum, &t);
+  if (b < nb) {
+    s.start[b] = ex;
+    s.run[b] += ex;
+  }
+  if (threadIdx.x == 0) s.start[nb] = t;
+  __syncthreads();
+  if (tail) {
+    plan_tail(p, s);
+    return;
+  }
+  wide_scatter(lo, hi, nb, key, s.run, s.masks, [&](int i, int bk, int pos) {
+    p.sorted[pos] = i;
+    if (p.sort_order_out && bk < p.E) p.sort_order_out[pos] = routed_slot(p, i);
+  });
+}
+
+// Larger batches: the same plan over RB-slot blocks in three launches --
 // per-block bucket counts, one work-group that turns them into per-block
 // bucket offsets (block order keeps every bucket in ascending slot order)
 // and runs the tail, and a per-block stable scatter from those offsets.
@@ -618,6 +666,12 @@ int launch_route_plan(const RoutePlanParams& p, hipStream_t stream) {
   if (nblk == 0 || p.blk_cnt == nullptr) {
     hipLaunchKernelGGL(route_plan_kernel, dim3(1), dim3(RT), 0, stream, p);
     return check_launch("route_plan_kernel");
+  }
+  if (p.n <= kRecountMaxSlots) {
+    int grid, per;
+    wide_grid(p.n, &grid, &per);
+    hipLaunchKernelGGL(route_plan_recount_kernel, dim3(grid + 1), dim3(RT), 0, stream, p, per);
+    return check_launch("route_plan_recount_kernel");
   }
   hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)nblk), dim3(RT), 0, stream, p);
   int st = check_launch("route_count_kernel");
