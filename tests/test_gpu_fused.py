@@ -321,6 +321,49 @@ def test_fused_duplicate_ids_randint_routing(T, device):
     assert_close_rel(out, ref, TOL, f"duplicate ids T={T}")
 
 
+def _counts_routing(counts, T, k, seed):
+    """[T, k] ids in which expert j takes counts[j] slots (sum = T * k) and no
+    token repeats an expert: the sorted labels fill the columns one after
+    another, so an expert's run covers distinct tokens."""
+    labels = np.repeat(np.arange(len(counts)), counts)
+    assert labels.size == T * k and max(counts) <= T
+    ids = labels.reshape(k, T).T.copy()
+    rng = np.random.default_rng(seed)
+    for t in range(T):
+        rng.shuffle(ids[t])
+    return ids
+
+
+@pytest.mark.parametrize("T,k,counts", [
+    (64, 4, [64, 49, 33, 17, 48, 32, 12, 1]),      # 4, 4, 3, 2, 3, 2, 1, 1 tiles
+    (48, 4, [48, 47, 31, 17, 16, 15, 10, 8]),      # 3, 3, 2, 2, 1, 1, 1, 1
+    (40, 2, [40, 24, 16]),                          # 3, 2, 1
+])
+def test_fused_multi_tile_experts(T, k, counts, device):
+    """Experts with 17-64 rows: a gate/up unit of the LDS path then covers two
+    to four 16-row tiles over one copy of its weight slice (pairs of waves or
+    single waves per tile instead of the four-way k-split).  Shape H=2048,
+    I=768 (Qwen3's), 16 experts."""
+    from exq_amd.kernels import fused_experts
+    banner(f"fused multi-tile experts T={T} counts={counts}")
+    E, I, H = 16, 768, 2048
+    p13, s13, p2, s2 = _pack_gpu(E, I, H, 41, device)
+    ids = _counts_routing(counts, T, k, T)
+    w = np.random.default_rng(T + 1).random((T, k)).astype(np.float32)
+    x = _hidden(T, H, 9, device)
+    for ids_dt in (torch.int64, torch.int32):
+        out = fused_experts(x, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                            torch.from_numpy(ids).to(ids_dt).to(device))
+        ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+        assert_close_rel(out, ref, TOL, f"multi-tile T={T} {ids_dt}")
+    # fp16 activations
+    xh = x.to(torch.float16)
+    out = fused_experts(xh, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                        torch.from_numpy(ids).to(device))
+    assert_close_rel(out, oracle_int4_layer(xh, p13, s13, p2, s2, ids, w), TOL,
+                     f"multi-tile T={T} fp16")
+
+
 def test_unsort_output_inverts_grouped_gemm(device):
     """unsort_output(moe_grouped_gemm(...)) is the reference's
     pytorch_moe_reference composition (moe_grouped_gemm.py:234-290): the
