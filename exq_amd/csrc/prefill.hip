@@ -246,6 +246,34 @@ __device__ __forceinline__ void tile_store(const GemmArgs& a, const TgEntry& te,
   }
 }
 
+// Scheduling-group hints for one software-pipelined k-step: NM MFMAs, ND LDS
+// reads and NV VALU instructions in eight groups of (MFMAs, one read, VALU).
+template <int NM, int ND, int NV>
+__device__ __forceinline__ void tile_interleave_hint() {
+  constexpr int G = 8;
+  static_assert(NM % G == 0 && ND <= G, "groups");
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, NM / G, 0);  // MFMA
+    if (i < ND) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x002, (NV + G - 1) / G, 0);  // VALU
+  }
+}
+
+// Hints for the last k-step of a chunk: NM MFMAs with the NV scaling VALU
+// instructions one MFMA pair behind (each pair's products are ready by the
+// time its scaling issues).
+template <int NM, int NV>
+__device__ __forceinline__ void tile_scale_hint() {
+  constexpr int G = NM / 2;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    if (i > 0) __builtin_amdgcn_sched_group_barrier(0x002, NV / G, 0);  // VALU
+  }
+  __builtin_amdgcn_sched_group_barrier(0x002, NV - (G - 1) * (NV / G), 0);
+}
+
 // The four waves are one row of the tile (1 x 4): each wave holds all TM =
 // 16 MT token rows and NTW 16-row weight tiles, so TN = 64 NTW.
 //   MT = 8, NTW = 2: 128 x 128 (each dequantised weight fragment feeds 8 MFMAs);
@@ -366,6 +394,12 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
 #pragma unroll
     for (int t = 0; t < NTW; ++t) tot[mt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+  // One chunk (= one scale group): the accumulators start from the base
+  // correction and end scaled into tot.  Software-pipelined by k-step: while
+  // step s's MT x NTW MFMAs issue, step s + 1's activation fragments are read
+  // from LDS and its weight fragments dequantised (both independent of the
+  // MFMAs in flight), and scheduling-group hints interleave the three streams
+  // so that the VALU and LDS work issues in the matrix pipe's shadow.
 #define EXQ_TILE_CHUNK(ST, FIRST, LAST)                                                      \
   do {                                                                                       \
     const unsigned char* A_ = ST ? sA1 : sA0;                                                \
@@ -374,30 +408,43 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
     uint4 bw[NTW];                                                                           \
     _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                          \
         bw[t] = *reinterpret_cast<const uint4*>(B_ + boff + (brow(t) - brow(0)) * 64);      \
-    f32x4_t cin[MT];                                                                         \
-    if (FIRST) {                                                                             \
-      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
-          _Pragma("unroll") for (int v_ = 0; v_ < 4; ++v_)                                   \
-              cin[mt][v_] = row_bcast(rs_raw[ST][mt >> 2], (mt & 3) * 4 + v_);               \
+    _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) {                                      \
+      f32x4_t c_;                                                                            \
+      _Pragma("unroll") for (int v_ = 0; v_ < 4; ++v_)                                       \
+          c_[v_] = FIRST ? row_bcast(rs_raw[ST][mt >> 2], (mt & 3) * 4 + v_) : 0.f;          \
+      _Pragma("unroll") for (int t = 0; t < NTW; ++t) acc[mt][t] = c_;                       \
     }                                                                                        \
+    uint4 afp[2][MT], bfp[2][NTW];                                                           \
+    _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                        \
+        afp[0][mt] = *reinterpret_cast<const uint4*>(A_ + aoff + mt * 16 * 256);             \
+    _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                          \
+        bfp[0][t] = deq_nat(bw[t].x, dq_mask, dq_magic);                                     \
+    __builtin_amdgcn_sched_barrier(0);                                                       \
     _Pragma("unroll") for (int s = 0; s < 4; ++s) {                                          \
-      uint4 af[MT];                                                                          \
-      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
-          af[mt] = *reinterpret_cast<const uint4*>(A_ + (aoff ^ (s * 16)) + mt * 16 * 256);  \
-      uint4 bf[NTW];                                                                         \
-      _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                      \
-        const uint32_t p_ = s == 0 ? bw[t].x : s == 1 ? bw[t].y : s == 2 ? bw[t].z : bw[t].w; \
-        bf[t] = deq_nat(p_, dq_mask, dq_magic);                                              \
+      const int c_ = s & 1, n_ = c_ ^ 1;                                                     \
+      if (s < 3) {                                                                           \
+        _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                    \
+            afp[n_][mt] =                                                                    \
+                *reinterpret_cast<const uint4*>(A_ + (aoff ^ ((s + 1) * 16)) + mt * 16 * 256); \
+        _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                    \
+          const uint32_t p_ = s == 0 ? bw[t].y : s == 1 ? bw[t].z : bw[t].w;                 \
+          bfp[n_][t] = deq_nat(p_, dq_mask, dq_magic);                                       \
+        }                                                                                    \
       }                                                                                      \
       _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
           _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                    \
-              acc[mt][t] = mfma16<BF>(af[mt], bf[t], (FIRST && s == 0) ? cin[mt] : acc[mt][t]); \
-    }                                                                                        \
-    if (LAST) {                                                                              \
-      _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                      \
-        const float sc_ = f16_bits_to_f32(sc_raw[ST][t]);                                    \
-        _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) tot[mt][t] += sc_ * acc[mt][t];    \
+              acc[mt][t] = mfma16<BF>(afp[c_][mt], bfp[c_][t], acc[mt][t]);                  \
+      if (s < 3) {                                                                           \
+        tile_interleave_hint<MT * NTW, MT, 9 * NTW>();                                       \
+      } else if (LAST) {                                                                     \
+        /* each accumulator's scaling follows its last MFMA, under the later ones */         \
+        _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                    \
+          const float sc_ = f16_bits_to_f32(sc_raw[ST][t]);                                  \
+          _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) tot[mt][t] += sc_ * acc[mt][t];  \
+        }                                                                                    \
+        tile_scale_hint<MT * NTW, 4 * MT * NTW + NTW>();                                     \
       }                                                                                      \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
     }                                                                                        \
   } while (0)
 
