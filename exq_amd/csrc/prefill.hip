@@ -260,6 +260,21 @@ __device__ __forceinline__ void tile_interleave_hint() {
   }
 }
 
+// The same for the first k-step, which also issues the next chunk's NL copies
+// and loads.
+template <int NM, int ND, int NV, int NL>
+__device__ __forceinline__ void tile_interleave_hint_vm() {
+  constexpr int G = 8;
+  static_assert(NM % G == 0 && ND <= G, "groups");
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, NM / G, 0);  // MFMA
+    if (i < ND) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    __builtin_amdgcn_sched_group_barrier(0x002, (NV + G - 1) / G, 0);  // VALU
+    __builtin_amdgcn_sched_group_barrier(0x020, (NL + G - 1) / G, 0);  // VMEM read
+  }
+}
+
 // Hints for the last k-step of a chunk: NM MFMAs with the NV scaling VALU
 // instructions one MFMA pair behind (each pair's products are ready by the
 // time its scaling issues).
@@ -400,20 +415,13 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   // from LDS and its weight fragments dequantised (both independent of the
   // MFMAs in flight), and scheduling-group hints interleave the three streams
   // so that the VALU and LDS work issues in the matrix pipe's shadow.
-#define EXQ_TILE_CHUNK(ST, FIRST, LAST)                                                      \
+#define EXQ_TILE_CHUNK(ST, PF)                                                               \
   do {                                                                                       \
     const unsigned char* A_ = ST ? sA1 : sA0;                                                \
     const unsigned char* B_ = ST ? sB1 : sB0;                                                \
-    f32x4_t acc[MT][NTW];                                                                    \
     uint4 bw[NTW];                                                                           \
     _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                          \
         bw[t] = *reinterpret_cast<const uint4*>(B_ + boff + (brow(t) - brow(0)) * 64);      \
-    _Pragma("unroll") for (int mt = 0; mt < MT; ++mt) {                                      \
-      f32x4_t c_;                                                                            \
-      _Pragma("unroll") for (int v_ = 0; v_ < 4; ++v_)                                       \
-          c_[v_] = FIRST ? row_bcast(rs_raw[ST][mt >> 2], (mt & 3) * 4 + v_) : 0.f;          \
-      _Pragma("unroll") for (int t = 0; t < NTW; ++t) acc[mt][t] = c_;                       \
-    }                                                                                        \
     uint4 afp[2][MT], bfp[2][NTW];                                                           \
     _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                        \
         afp[0][mt] = *reinterpret_cast<const uint4*>(A_ + aoff + mt * 16 * 256);             \
@@ -434,9 +442,12 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
       _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
           _Pragma("unroll") for (int t = 0; t < NTW; ++t)                                    \
               acc[mt][t] = mfma16<BF>(afp[c_][mt], bfp[c_][t], acc[mt][t]);                  \
-      if (s < 3) {                                                                           \
+      if (s == 0) {                                                                          \
+        PF;                                                                                  \
+        tile_interleave_hint_vm<MT * NTW, MT, 9 * NTW, QA + QB + NTW + RSR>();               \
+      } else if (s < 3) {                                                                    \
         tile_interleave_hint<MT * NTW, MT, 9 * NTW>();                                       \
-      } else if (LAST) {                                                                     \
+      } else {                                                                               \
         /* each accumulator's scaling follows its last MFMA, under the later ones */         \
         _Pragma("unroll") for (int t = 0; t < NTW; ++t) {                                    \
           const float sc_ = f16_bits_to_f32(sc_raw[ST][t]);                                  \
@@ -452,17 +463,31 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   // from the base correction and end scaled into tot.
   // The scheduling barriers keep each prefetch at the head of its chunk (the
   // scheduler would otherwise sink the loads into the MFMA stream).
+  // Per chunk: wait for this wave's copies of the chunk (and its row sums),
+  // set the accumulators to the chunk's base correction (registers only, so
+  // before the barrier), then the barrier; the next chunk's copies go out
+  // inside the first k-step, among its MFMAs.
+  f32x4_t acc[MT][NTW];
+  auto start_chunk = [&](int st) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4_t c_;
+#pragma unroll
+      for (int v_ = 0; v_ < 4; ++v_) c_[v_] = row_bcast(rs_raw[st][mt >> 2], (mt & 3) * 4 + v_);
+#pragma unroll
+      for (int t = 0; t < NTW; ++t) acc[mt][t] = c_;
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
   prefetch(0, 0);
   for (int ch = 0; ch < nch; ch += 2) {
-    chunk_barrier();
-    prefetch(1, ch + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    EXQ_TILE_CHUNK(0, true, true);
+    start_chunk(0);
+    EXQ_TILE_CHUNK(0, prefetch(1, ch + 1));
     if (ch + 1 >= nch) break;
-    chunk_barrier();
-    prefetch(0, ch + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    EXQ_TILE_CHUNK(1, true, true);
+    start_chunk(1);
+    EXQ_TILE_CHUNK(1, prefetch(0, ch + 2));
   }
 #undef EXQ_TILE_CHUNK
   wait_vm_all();  // the last (empty) prefetch has drained before the work-group ends
