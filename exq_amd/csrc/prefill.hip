@@ -462,10 +462,6 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
     }                                                                                        \
   } while (0)
 
-  // One chunk is one scale group (group_size 128): each chunk's sums start
-  // from the base correction and end scaled into tot.
-  // The scheduling barriers keep each prefetch at the head of its chunk (the
-  // scheduler would otherwise sink the loads into the MFMA stream).
   // Per chunk: wait for this wave's copies of the chunk (and its row sums),
   // set the accumulators to the chunk's base correction (registers only, so
   // before the barrier), then the barrier; the next chunk's copies go out
