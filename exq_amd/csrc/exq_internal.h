@@ -73,12 +73,17 @@ bool tile_gemm_applies(int tier, int mode, int n_rows, int inter, int K, int gro
 // The INT4 tiles can be 64 expert-sorted rows x 256 weight rows instead (token
 // groups of kTokenGroup rows): GATEUP needs I % 128 == 0, DOWN / PLAIN rows % 256.
 bool tile_gemm_wide_applies(int mode, int n_rows, int inter);
+// INT4 tile shapes: 128 x 128 and 64 x 256 (per-group accumulators, base
+// corrections from launch_group_rowsum), and 128 x 256 with scaled weight
+// operands (token groups of kTokenGroupI4 rows, same row conditions as 64 x
+// 256; needs no row sums).
+enum TileShape { TILE_128x128 = 0, TILE_64x256 = 1, TILE_PS_128x256 = 2 };
 int64_t tile_rowsum_floats(int64_t rows, int64_t K);
 int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows, int K, int gs,
                         float* out, hipStream_t s);
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
                      int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s,
-                     bool wide = false);
+                     int shape = TILE_128x128);
 
 // INT4 grouped GEMMs for the shapes outside the tiled / grouped kernels
 // (general.hip): K % 32 == 0, a group size that is a multiple of 32 dividing

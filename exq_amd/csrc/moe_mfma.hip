@@ -577,17 +577,21 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   const bool tile_bf = tier != nullptr && x32 &&
                        tile_gemm_applies(0, MODE_GATEUP, 2 * I, I, H, gs) &&
                        tile_gemm_applies(0, MODE_DOWN, H, I, I, gs);
-  // INT4 tiles of 64 sorted rows x 256 weight rows when both projections take
-  // them and the routed experts average fewer than 512 rows: the same MFMA
-  // work per chunk from fewer bytes of copies, and about half the padding rows
-  // of 128-row groups (DeepSeek-V2-Lite at 2048 tokens, 192 rows per expert:
-  // 627 -> 585 us).  With more rows per expert there is little padding to save
-  // and the 128 x 128 tile's 8 MFMAs per dequantised weight fragment win
-  // (Mixtral at 4096 tokens, 1024 rows per expert: 3518 -> 3612 us wide).
-  const bool wide = tile && tile_gemm_wide_applies(MODE_GATEUP, 2 * I, I) &&
-                    tile_gemm_wide_applies(MODE_DOWN, H, I) &&
-                    (int64_t)T * k < 512 * (int64_t)E;
-  rp.i4_group = tile ? (wide ? kTokenGroup : kTokenGroupI4) : kTokenGroup;
+  // INT4 tile shape, when both projections take the 256-row tiles:
+  // * experts averaging fewer than 512 routed rows: 64 sorted rows x 256 weight
+  //   rows, the same MFMA work per chunk from fewer bytes of copies and about
+  //   half the padding rows of 128-row groups (DeepSeek-V2-Lite at 2048 tokens,
+  //   192 rows per expert: 627 -> 585 us against 128 x 128);
+  // * more rows per expert: 128 x 256 with scaled weight operands, each
+  //   activation chunk feeding twice the weight rows of a 128 x 128 tile
+  //   (Mixtral at 4096 tokens, 1024 rows per expert: 3310 -> 3044 us; 128-row
+  //   groups would pad DeepSeek's experts: 560 -> 579 us there).
+  // Otherwise 128 x 128.
+  const bool wide_ok = tile && tile_gemm_wide_applies(MODE_GATEUP, 2 * I, I) &&
+                       tile_gemm_wide_applies(MODE_DOWN, H, I);
+  const int shape = !wide_ok ? TILE_128x128
+                             : ((int64_t)T * k < 512 * (int64_t)E ? TILE_64x256 : TILE_PS_128x256);
+  rp.i4_group = tile ? (shape == TILE_64x256 ? kTokenGroup : kTokenGroupI4) : kTokenGroup;
   rp.bf_group = tile_bf ? kTokenGroupI4 : kTokenGroup;
   rp.counters = nullptr;
   rp.n_counters = 0;
@@ -710,9 +714,11 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       if (st) return st;
     }
     if (run_tile) {
-      st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
-      if (st) return st;
-      st = launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s, wide);
+      if (shape != TILE_PS_128x256) {
+        st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
+        if (st) return st;
+      }
+      st = launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s, shape);
       if (st) return st;
     }
     st = record_stage(2, s);
@@ -736,9 +742,11 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       if (st) return st;
     }
     if (run_tile) {
-      st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
-      if (st) return st;
-      st = launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s, wide);
+      if (shape != TILE_PS_128x256) {
+        st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
+        if (st) return st;
+      }
+      st = launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s, shape);
       if (st) return st;
     }
   }

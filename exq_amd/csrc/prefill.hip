@@ -494,6 +494,332 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
   tile_store<BF, MODE, MT, NTW, TN>(a, te, nt, wm, wn, r16, kq, tot);
 }
 
+// ---- INT4 experts, scaled weight operands ------------------------------------
+// 128 sorted rows x 256 weight rows per work-group, four waves of 128 x 64
+// (4 x 2 MFMA 32x32x16 tiles).  Each weight fragment is dequantised with its
+// group scale applied, (n - 8) * s rounded once to the operand type (for f16
+// operands this is the value the reference's kernel multiplies,
+// moe_int4_kernel.py:211-233), so the fp32 accumulators run over the whole
+// contraction: no per-group accumulator set, no base correction and no row-sum
+// pass.  That halves the accumulator registers per output, which is what lets
+// a wave hold 128 x 64 outputs at two waves per SIMD: every activation chunk
+// copied into LDS feeds 256 weight rows, twice the 128 x 128 tile's reuse.
+//
+// Data movement: activations in 64-k chunks (128 rows x 128 B, 16 KiB), packed
+// weights one scale group at a time (256 rows x 64 B, 16 KiB), both double
+// buffered (64 KiB per work-group, two work-groups per CU): the next
+// activation chunk is copied during the current one, the next group's weights
+// during the first chunk of the current group, two chunks ahead of their use.
+//
+// MFMA 32x32x16 operands: lane l holds row / column l % 32 and 8 k values of
+// half h = l / 32.  At k-step s (four per chunk) of chunk half c of a group,
+// lane half h covers group-relative k = 64 c + 32 h + 8 s + i, so a lane's
+// packed bytes for a whole chunk are 16 consecutive bytes (one ds_read_b128
+// per weight tile and chunk), and its activation fragment for step s is 16
+// consecutive bytes of the staged row.
+constexpr int PS_KC = 64;                    // activation chunk (k)
+constexpr int PS_A_STAGE = 128 * PS_KC * 2;  // 16 KiB
+constexpr int PS_B_STAGE = 256 * 64;         // 256 weight rows x one 128-k group
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Swizzles for the 32-lane operand rows (same bank-group rule as above: each
+// group of 16 lanes served together covers 16 distinct 16-byte units).
+//   activation rows (128 B, 8 columns): c ^ psa_swz(r)
+//   packed weight rows (64 B, 4 columns): c ^ psb_swz(r)
+__device__ __forceinline__ int psa_swz(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int psb_swz(int r) { return (r >> 2) & 3; }
+
+template <bool BF>
+__device__ __forceinline__ f32x16_t mfma32(const uint4& a, const uint4& b, f32x16_t c) {
+  if constexpr (BF) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+// Per-lane scale constants of one weight row and group.
+struct PsScale {
+  float s, s16, c;  // bf16: s, s / 16, -8 s
+  uint32_t s2;      // f16: s in both halves
+};
+
+template <bool BF>
+__device__ __forceinline__ PsScale ps_scale(uint32_t raw) {
+  PsScale p;
+  if constexpr (BF) {
+    p.s = f16_bits_to_f32(raw & 0xffffu);
+    p.s16 = p.s * 0.0625f;
+    p.c = -8.0f * p.s;
+    p.s2 = 0;
+  } else {
+    p.s = p.s16 = p.c = 0.f;
+    p.s2 = __builtin_amdgcn_perm(raw, raw, 0x01000100u);
+  }
+  return p;
+}
+
+// 8 packed nibbles (k offsets 0..7, low nibble = even k) -> the 8 operand
+// values (n - 8) * s in natural k order.
+//   bf16: the exact product in fp32 (n from v_cvt_f32_ubyte*, the high nibbles
+//         as 16 n against s / 16), one rounding by v_cvt_pk_bf16_f32;
+//   f16:  the exact 1024 + n pair (v_perm_b32 + v_and_or_b32), minus 1032
+//         (exact), times s: one f16 rounding, the reference's product.
+template <bool BF>
+__device__ __forceinline__ uint4 deq_scaled(uint32_t p, const PsScale& sc, uint32_t mask,
+                                            uint32_t magic) {
+  uint4 o;
+  if constexpr (BF) {
+    uint32_t lo = p & 0x0F0F0F0Fu, hi = p & 0xF0F0F0F0u;
+    asm volatile("" : "+v"(lo), "+v"(hi));  // keep whole-byte conversions (v_cvt_f32_ubyteN)
+    auto pk = [](float a, float b) {
+      const f32x2_t v = {a, b};
+      return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+    };
+    o.x = pk(__builtin_fmaf((float)(lo & 0xffu), sc.s, sc.c),
+             __builtin_fmaf((float)(hi & 0xffu), sc.s16, sc.c));
+    o.y = pk(__builtin_fmaf((float)((lo >> 8) & 0xffu), sc.s, sc.c),
+             __builtin_fmaf((float)((hi >> 8) & 0xffu), sc.s16, sc.c));
+    o.z = pk(__builtin_fmaf((float)((lo >> 16) & 0xffu), sc.s, sc.c),
+             __builtin_fmaf((float)((hi >> 16) & 0xffu), sc.s16, sc.c));
+    o.w = pk(__builtin_fmaf((float)(lo >> 24), sc.s, sc.c),
+             __builtin_fmaf((float)(hi >> 24), sc.s16, sc.c));
+  } else {
+    const uint4 e = deq_nat(p, mask, magic);  // 1024 + n
+    const f16x2_t off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const f16x2_t s2 = __builtin_bit_cast(f16x2_t, sc.s2);
+    o.x = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2_t, e.x) + off) * s2);
+    o.y = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2_t, e.y) + off) * s2);
+    o.z = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2_t, e.z) + off) * s2);
+    o.w = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2_t, e.w) + off) * s2);
+  }
+  return o;
+}
+
+// First LDS weight row of 32-row tile t (0, 1) of wave wn.  GATEUP: tile 0 the
+// gate rows j0 + 32 wn.., tile 1 the matching up rows (LDS rows 128..).
+template <int MODE>
+__device__ __forceinline__ int ps_brow(int wn, int t) {
+  if constexpr (MODE == MODE_GATEUP)
+    return t * 128 + wn * 32;
+  else
+    return wn * 64 + t * 32;
+}
+
+template <bool BF, int MODE>
+__global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta) {
+  constexpr int MT = 4, NT = 2, TN = 256;
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[PS_A_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[PS_A_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[PS_B_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[PS_B_STAGE];
+
+  TgEntry te;
+  int nt;
+  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, te, nt)) return;  // INT4 groups
+  const int cnt = te.cnt, pos0 = te.pos0;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r32 = lane & 31, h = lane >> 5;
+  const int wn = wave;
+  const int K = a.K;
+  const int nch = K / PS_KC;  // activation chunks, two per scale group
+  const int ngs = K / KC;     // scale groups (group_size == 128)
+
+  const int widx = a.w.index ? a.w.index[te.e] : te.e;
+  const int64_t ebase = (int64_t)widx * a.n_rows;
+  const int rowbytes = K / 2;
+  auto wrow = [&](int rho) { return tile_wrow<MODE, TN>(a, nt, rho); };
+  auto x_row = [&](int m) { return tile_xrow<MODE>(a, te, m); };
+
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(a.w.i4 + ebase * rowbytes, (int64_t)a.n_rows * rowbytes);
+  const __amdgpu_buffer_rsrc_t sr =
+      make_rsrc(a.w.i4_scales + ebase * ngs, (int64_t)a.n_rows * ngs * 2);
+  const __amdgpu_buffer_rsrc_t xr =
+      MODE == MODE_GATEUP
+          ? make_rsrc(a.x, ta.x_bytes)
+          : make_rsrc(a.x + (int64_t)pos0 * a.x_stride, (int64_t)cnt * a.x_stride * 2);
+  const __amdgpu_buffer_rsrc_t wnull = make_rsrc(a.w.i4, 0);
+  const __amdgpu_buffer_rsrc_t snull = make_rsrc(a.w.i4_scales, 0);
+  const __amdgpu_buffer_rsrc_t xnull = make_rsrc(a.x, 0);
+
+  // ---- per-lane DMA offsets ------------------------------------------------
+  // activations: instruction q fills LDS rows 8j..8j+7 (j = 4 wave + q), 8 columns each;
+  // weights: instruction q fills LDS rows 16j..16j+15, 4 columns each.
+  int voffA[4], voffB[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int m = (wave * 4 + q) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ psa_swz(m);
+    const int xrow = x_row(m);
+    voffA[q] = (MODE == MODE_GATEUP ? xrow : xrow - pos0) * (int)a.x_stride * 2 + c * 16;
+    const int rho = (wave * 4 + q) * 16 + (lane >> 2);
+    const int cb = (lane & 3) ^ psb_swz(rho);
+    voffB[q] = wrow(rho) * rowbytes + cb * 16;
+  }
+  // Scale of weight row wrow(ps_brow(t) + r32): lane part + a wave-uniform delta.
+  const int soffS = wrow(ps_brow<MODE>(wn, 0) + r32) * ngs * 2;
+  int sdel[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    sdel[t] = __builtin_amdgcn_readfirstlane(
+        (wrow(ps_brow<MODE>(wn, t) + r32) - wrow(ps_brow<MODE>(wn, 0) + r32)) * ngs * 2);
+
+  // LDS read offsets: A fragment of m-tile mt, k-step s = aoff ^ (16 s) + 4 KiB mt;
+  // weight tile t, chunk half c = (boff + brow(t) * 64) ^ (32 c).
+  const int aoff = r32 * 128 + ((4 * h) ^ psa_swz(r32)) * 16;
+  const int boff = r32 * 64 + (h ^ psb_swz(r32)) * 16;
+  uint32_t sc_raw[NT];
+
+  auto prefetch_a = [&](int st, int ch) {
+    const bool ok = ch < nch;
+    const int chl = ok ? ch : 0;
+    unsigned char* A = st ? sA1 : sA0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma16(ok ? xr : xnull, A + (wave * 4 + q) * 1024, voffA[q], chl * 128);
+  };
+  auto prefetch_b = [&](int st, int g) {
+    const bool ok = g < ngs;
+    const int gl = ok ? g : 0;
+    unsigned char* B = st ? sB1 : sB0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma16(ok ? wr : wnull, B + (wave * 4 + q) * 1024, voffB[q], gl * 64);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      sc_raw[t] = __builtin_amdgcn_raw_buffer_load_b16(ok ? sr : snull, soffS, gl * 2 + sdel[t], 0);
+  };
+
+  const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
+  uint32_t dq_magic = 0x64006400u;
+  asm volatile("" : "+v"(dq_magic));
+
+  constexpr int PS_DQ_VALU = BF ? 22 : 17;  // VALU instructions per dequantised fragment
+  f32x16_t acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mt][t][v] = 0.f;
+
+  // Copies in flight: the next activation chunk, and the weights and scales
+  // of the next group from the first chunk of a group on (two chunks ahead).
+  // Each wave issues 4 copies per activation chunk and 4 copies + NT scale
+  // loads per group, so a chunk's own copies have landed when none (first
+  // chunk of a group) or 4 + NT (second) of the wave's later loads are
+  // outstanding.
+  PsScale sc[NT];
+  auto start_chunk = [&](int half) {
+    if (half == 0)
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory");
+    if (half == 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) sc[t] = ps_scale<BF>(sc_raw[t]);
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  static_assert(NT == 2, "the wait count above assumes 4 + NT = 6");
+
+  // One 64-k chunk: activation stage AS, weight stage BS, half HF of the group.
+#define EXQ_PS_CHUNK(AS, BS, HF, PF)                                                         \
+  do {                                                                                       \
+    const unsigned char* A_ = AS ? sA1 : sA0;                                                \
+    const unsigned char* B_ = BS ? sB1 : sB0;                                                \
+    uint4 bw[NT];                                                                            \
+    _Pragma("unroll") for (int t = 0; t < NT; ++t)                                           \
+        bw[t] = *reinterpret_cast<const uint4*>(                                             \
+            B_ + ((boff + ps_brow<MODE>(wn, t) * 64) ^ (32 * HF)));                          \
+    uint4 af[2][MT], wf[2][NT];                                                              \
+    _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                        \
+        af[0][mt] = *reinterpret_cast<const uint4*>(A_ + aoff + mt * 32 * 128);              \
+    _Pragma("unroll") for (int t = 0; t < NT; ++t)                                           \
+        wf[0][t] = deq_scaled<BF>(bw[t].x, sc[t], dq_mask, dq_magic);                        \
+    __builtin_amdgcn_sched_barrier(0);                                                       \
+    _Pragma("unroll") for (int s = 0; s < 4; ++s) {                                          \
+      const int c_ = s & 1, n_ = c_ ^ 1;                                                     \
+      if (s < 3) {                                                                           \
+        _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                    \
+            af[n_][mt] =                                                                     \
+                *reinterpret_cast<const uint4*>(A_ + (aoff ^ ((s + 1) * 16)) + mt * 32 * 128); \
+        _Pragma("unroll") for (int t = 0; t < NT; ++t) {                                     \
+          const uint32_t p_ = s == 0 ? bw[t].y : s == 1 ? bw[t].z : bw[t].w;                 \
+          wf[n_][t] = deq_scaled<BF>(p_, sc[t], dq_mask, dq_magic);                          \
+        }                                                                                    \
+      }                                                                                      \
+      _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
+          _Pragma("unroll") for (int t = 0; t < NT; ++t)                                     \
+              acc[mt][t] = mfma32<BF>(af[c_][mt], wf[c_][t], acc[mt][t]);                    \
+      if (s == 0) {                                                                          \
+        PF;                                                                                  \
+        tile_interleave_hint_vm<MT * NT, MT, PS_DQ_VALU * NT, HF ? 4 : 8 + NT>();             \
+      } else if (s < 3) {                                                                    \
+        tile_interleave_hint<MT * NT, MT, PS_DQ_VALU * NT>();                                 \
+      }                                                                                      \
+      __builtin_amdgcn_sched_barrier(0);                                                     \
+    }                                                                                        \
+  } while (0)
+
+  // One scale group = two activation chunks.  The weight stage is a constant
+  // in each copy of the group body (two groups per iteration, an odd last
+  // group after the loop) so that the compiler can tell the stages apart and
+  // does not wait for the other stage's copies before reading this one.
+#define EXQ_PS_GROUP(G, BS)                                                                  \
+  do {                                                                                       \
+    start_chunk(0);                                                                          \
+    EXQ_PS_CHUNK(0, BS, 0, (prefetch_a(1, 2 * (G) + 1), prefetch_b((BS) ^ 1, (G) + 1)));     \
+    start_chunk(1);                                                                          \
+    EXQ_PS_CHUNK(1, BS, 1, prefetch_a(0, 2 * (G) + 2));                                      \
+  } while (0)
+  prefetch_a(0, 0);
+  prefetch_b(0, 0);
+  int g = 0;
+  for (; g + 1 < ngs; g += 2) {
+    EXQ_PS_GROUP(g, 0);
+    EXQ_PS_GROUP(g + 1, 1);
+  }
+  if (g < ngs) EXQ_PS_GROUP(g, 0);
+#undef EXQ_PS_GROUP
+#undef EXQ_PS_CHUNK
+  wait_vm_all();  // the last (empty) prefetch has drained before the work-group ends
+
+  // Output: accumulator v of tile (mt, t) is row 32 mt + 8 (v / 4) + 4 h + v % 4,
+  // column r32 of the tile.
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = mt * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+      if (m >= cnt) continue;
+      const int pos = pos0 + m;
+      if constexpr (MODE == MODE_GATEUP) {
+        uint16_t* mid = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride +
+                        nt * (TN / 2) + wn * 32 + r32;
+        *mid = (uint16_t)to_act_bits<BF>(silu_f32(acc[mt][0][v]) * acc[mt][1][v]);
+      } else if constexpr (MODE == MODE_PLAIN) {
+        uint16_t* c = reinterpret_cast<uint16_t*>(a.out) + (int64_t)pos * a.out_stride + nt * TN +
+                      wn * 64 + r32;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) c[t * 32] = (uint16_t)to_act_bits<BF>(acc[mt][t][v]);
+      } else {
+        const int slot = a.row_slot[pos];
+        float* part = reinterpret_cast<float*>(a.out) + (int64_t)slot * a.out_stride + nt * TN +
+                      wn * 64 + r32;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) part[t * 32] = acc[mt][t][v];
+      }
+    }
+  }
+}
+
 // ---- BF16 experts ------------------------------------------------------------
 // Same tile and unit order over the BF16 token groups [0, hdr[2]); chunks of
 // 64 k: activations and weights both 128 rows x 128 B per stage, swizzled in
@@ -676,7 +1002,7 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
 }
 
 template <int MODE>
-static int launch_tile_mode(int tier, bool bf, bool wide, const GemmArgs& a, const TileArgs& t,
+static int launch_tile_mode(int tier, bool bf, int shape, const GemmArgs& a, const TileArgs& t,
                             int64_t grid, hipStream_t s) {
   const dim3 g((unsigned)grid), b(TT);
   if (tier == 0) {
@@ -686,7 +1012,14 @@ static int launch_tile_mode(int tier, bool bf, bool wide, const GemmArgs& a, con
       hipLaunchKernelGGL((tile_gemm_bf16_kernel<false, MODE>), g, b, 0, s, a, t);
     return check_launch("tile_gemm_bf16_kernel");
   }
-  if (wide) {
+  if (shape == TILE_PS_128x256) {
+    if (bf)
+      hipLaunchKernelGGL((tile_ps_kernel<true, MODE>), g, b, 0, s, a, t);
+    else
+      hipLaunchKernelGGL((tile_ps_kernel<false, MODE>), g, b, 0, s, a, t);
+    return check_launch("tile_ps_kernel");
+  }
+  if (shape == TILE_64x256) {
     if (bf)
       hipLaunchKernelGGL((tile_gemm_kernel<true, MODE, 4, 4>), g, b, 0, s, a, t);
     else
@@ -706,21 +1039,21 @@ bool tile_gemm_wide_applies(int mode, int n_rows, int inter) {
 
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
                      int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s,
-                     bool wide) {
+                     int shape) {
   TileArgs t;
   t.rs = rs;
   t.rs_rows = (int)rs_rows;
   t.x_bytes = x_bytes;
-  wide = wide && tier == 2;
-  const int tn = wide ? 256 : 128;
+  if (tier != 2) shape = TILE_128x128;
+  const int tn = shape == TILE_128x128 ? 128 : 256;
   t.n_tiles = mode == MODE_GATEUP ? a.inter / (tn / 2) : a.n_rows / tn;
   const int64_t grid = 8 * cdiv(tg_cap, 8) * t.n_tiles;
   if (grid <= 0) return EXQ_SUCCESS;
   if (grid > INT32_MAX || rs_rows > INT32_MAX)
     return set_error(EXQ_ERROR_UNSUPPORTED, "tile_gemm: problem too large");
-  if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(tier, bf, wide, a, t, grid, s);
-  if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(tier, bf, wide, a, t, grid, s);
-  return launch_tile_mode<MODE_PLAIN>(tier, bf, wide, a, t, grid, s);
+  if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(tier, bf, shape, a, t, grid, s);
+  if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(tier, bf, shape, a, t, grid, s);
+  return launch_tile_mode<MODE_PLAIN>(tier, bf, shape, a, t, grid, s);
 }
 
 }  // namespace exq

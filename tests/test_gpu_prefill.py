@@ -22,6 +22,12 @@ WIDE = synth.MoeConfig("prefill_wide", 41, 1024, 512, 8, 2, True)
 # INT4 tiles are 128 rows x 128 weight rows (fewer rows per expert take the
 # 64 x 256 tiles, as WIDE does)
 FEW = synth.MoeConfig("prefill_few", 47, 1024, 512, 2, 2, True, zipf=False)
+# More than 512 rows per expert with 256-row tiles available: the INT4 tiles
+# are 128 rows x 256 weight rows with scaled weight operands.  ODD: three scale
+# groups in the down projection (I = 384), an odd count for the kernel's
+# two-groups-per-iteration loop; ONE: a single group (I = 128).
+PS_ODD = synth.MoeConfig("prefill_ps_odd", 49, 512, 384, 2, 2, True, zipf=False)
+PS_ONE = synth.MoeConfig("prefill_ps_one", 50, 256, 128, 2, 2, True, zipf=False)
 
 
 def _pack(E, I, H, seed, device, group_size=128):
@@ -38,7 +44,9 @@ def _hidden(T, H, seed, device, dtype):
 
 @pytest.mark.parametrize("cfg,T,dtype", [(WIDE, 300, torch.bfloat16), (WIDE, 300, torch.float16),
                                          (WIDE, 1100, torch.bfloat16), (FEW, 1100, torch.bfloat16),
-                                         (FEW, 1100, torch.float16)])
+                                         (FEW, 1100, torch.float16),
+                                         (PS_ODD, 700, torch.bfloat16), (PS_ODD, 700, torch.float16),
+                                         (PS_ONE, 600, torch.bfloat16), (PS_ONE, 600, torch.float16)])
 def test_prefill_fused_zipf_routing(cfg, T, dtype, device):
     from exq_amd.kernels import fused_experts
     banner(f"prefill fused {cfg.name} T={T} {dtype}")
@@ -131,6 +139,27 @@ def test_prefill_mixed_tiers(act, device):
                               torch.from_numpy(ids).to(device))
     from tests.test_gpu_mixed import _oracle
     assert_close_rel(out, _oracle(bank, x, ids, w), TOL, f"prefill mixed {act}")
+
+
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float16])
+def test_prefill_mixed_tiers_large_experts(act, device):
+    """A mixed bank with more than 512 rows per routed expert: its INT4
+    experts take the 128 x 256 scaled-operand tiles beside the BF16 tiles and
+    the grouped INT8 kernel."""
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    banner(f"prefill mixed tiers large experts {act}")
+    T, E = 1100, 8
+    cfg = synth.MoeConfig("mix_prefill_big", 51, 512, 256, E, 4, False)
+    assert T * cfg.top_k >= 512 * E
+    w13, w2 = synth.expert_weights_gpu(E, 256, 512, 73, device)
+    tiers = [2, 0, 2, 1, 2, 2, 1, 2]
+    bank = MixedExpertBank.from_weights(w13, w2, tiers, act_dtype=act)
+    ids, w = synth.routing(cfg, T)
+    x = _hidden(T, 512, 960, device, act)
+    out = fused_experts_mixed(x, bank, torch.from_numpy(w).to(device),
+                              torch.from_numpy(ids).to(device))
+    from tests.test_gpu_mixed import _oracle
+    assert_close_rel(out, _oracle(bank, x, ids, w), TOL, f"prefill mixed large experts {act}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
