@@ -584,8 +584,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   //   192 rows per expert: 627 -> 585 us against 128 x 128);
   // * more rows per expert: 128 x 256 with scaled weight operands, each
   //   activation chunk feeding twice the weight rows of a 128 x 128 tile
-  //   (Mixtral at 4096 tokens, 1024 rows per expert: 3310 -> 3044 us; 128-row
-  //   groups would pad DeepSeek's experts: 560 -> 579 us there).
+  //   (Mixtral at 4096 tokens, 1024 rows per expert: 3375 -> 3040 us against
+  //   128 x 128; 128-row groups would pad DeepSeek's experts: 560 -> 579 us).
   // Otherwise 128 x 128.
   const bool wide_ok = tile && tile_gemm_wide_applies(MODE_GATEUP, 2 * I, I) &&
                        tile_gemm_wide_applies(MODE_DOWN, H, I);

@@ -519,7 +519,7 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs t
 // consecutive bytes of the staged row.
 constexpr int PS_KC = 64;                    // activation chunk (k)
 constexpr int PS_A_STAGE = 128 * PS_KC * 2;  // 16 KiB
-constexpr int PS_B_STAGE = 256 * 64;         // 256 weight rows x one 128-k group
+constexpr int PS_B_ROW = 64;                 // one 128-k group of a packed weight row
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -600,19 +600,27 @@ __device__ __forceinline__ uint4 deq_scaled(uint32_t p, const PsScale& sc, uint3
   return o;
 }
 
-// First LDS weight row of 32-row tile t (0, 1) of wave wn.  GATEUP: tile 0 the
-// gate rows j0 + 32 wn.., tile 1 the matching up rows (LDS rows 128..).
-template <int MODE>
+// First LDS weight row of 32-row tile t (0, 1) of wave wn in a tile of TN
+// weight rows.  GATEUP: tile 0 the gate rows j0 + 32 wn.., tile 1 the matching
+// up rows (LDS rows TN / 2..).
+template <int MODE, int TN>
 __device__ __forceinline__ int ps_brow(int wn, int t) {
   if constexpr (MODE == MODE_GATEUP)
-    return t * 128 + wn * 32;
+    return t * (TN / 2) + wn * 32;
   else
     return wn * 64 + t * 32;
 }
 
+// Four waves of 128 x 64, two work-groups per CU.  (Eight waves of 128 x 64 in
+// one work-group per CU, each activation chunk feeding 512 weight rows,
+// measured 8 % slower for Mixtral: every chunk's barrier then holds all the
+// CU's waves.)
 template <bool BF, int MODE>
 __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta) {
-  constexpr int MT = 4, NT = 2, TN = 256;
+  constexpr int W = TT / 64;
+  constexpr int MT = 4, NT = 2, TN = 64 * W;
+  constexpr int QA = 16 / W;                    // activation copies per wave and chunk
+  constexpr int PS_B_STAGE = TN * PS_B_ROW;     // 4 weight copies per wave and group
   __shared__ __attribute__((aligned(1024))) unsigned char sA0[PS_A_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sA1[PS_A_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sB0[PS_B_STAGE];
@@ -650,26 +658,29 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
   const __amdgpu_buffer_rsrc_t xnull = make_rsrc(a.x, 0);
 
   // ---- per-lane DMA offsets ------------------------------------------------
-  // activations: instruction q fills LDS rows 8j..8j+7 (j = 4 wave + q), 8 columns each;
-  // weights: instruction q fills LDS rows 16j..16j+15, 4 columns each.
-  int voffA[4], voffB[4];
+  // activations: instruction q fills LDS rows 8j..8j+7 (j = QA wave + q), 8 columns each;
+  // weights: instruction q fills LDS rows 16j..16j+15 (j = 4 wave + q), 4 columns each.
+  int voffA[QA], voffB[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int m = (wave * 4 + q) * 8 + (lane >> 3);
+  for (int q = 0; q < QA; ++q) {
+    const int m = (wave * QA + q) * 8 + (lane >> 3);
     const int c = (lane & 7) ^ psa_swz(m);
     const int xrow = x_row(m);
     voffA[q] = (MODE == MODE_GATEUP ? xrow : xrow - pos0) * (int)a.x_stride * 2 + c * 16;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
     const int rho = (wave * 4 + q) * 16 + (lane >> 2);
     const int cb = (lane & 3) ^ psb_swz(rho);
     voffB[q] = wrow(rho) * rowbytes + cb * 16;
   }
   // Scale of weight row wrow(ps_brow(t) + r32): lane part + a wave-uniform delta.
-  const int soffS = wrow(ps_brow<MODE>(wn, 0) + r32) * ngs * 2;
+  const int soffS = wrow(ps_brow<MODE, TN>(wn, 0) + r32) * ngs * 2;
   int sdel[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
     sdel[t] = __builtin_amdgcn_readfirstlane(
-        (wrow(ps_brow<MODE>(wn, t) + r32) - wrow(ps_brow<MODE>(wn, 0) + r32)) * ngs * 2);
+        (wrow(ps_brow<MODE, TN>(wn, t) + r32) - wrow(ps_brow<MODE, TN>(wn, 0) + r32)) * ngs * 2);
 
   // LDS read offsets: A fragment of m-tile mt, k-step s = aoff ^ (16 s) + 4 KiB mt;
   // weight tile t, chunk half c = (boff + brow(t) * 64) ^ (32 c).
@@ -682,7 +693,7 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
     const int chl = ok ? ch : 0;
     unsigned char* A = st ? sA1 : sA0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dma16(ok ? xr : xnull, A + (wave * 4 + q) * 1024, voffA[q], chl * 128);
+    for (int q = 0; q < QA; ++q) dma16(ok ? xr : xnull, A + (wave * QA + q) * 1024, voffA[q], chl * 128);
   };
   auto prefetch_b = [&](int st, int g) {
     const bool ok = g < ngs;
@@ -690,16 +701,31 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
     unsigned char* B = st ? sB1 : sB0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) dma16(ok ? wr : wnull, B + (wave * 4 + q) * 1024, voffB[q], gl * 64);
+  };
+  auto prefetch_scales = [&](int g) {
+    const bool ok = g < ngs;
+    const int gl = ok ? g : 0;
 #pragma unroll
     for (int t = 0; t < NT; ++t)
       sc_raw[t] = __builtin_amdgcn_raw_buffer_load_b16(ok ? sr : snull, soffS, gl * 2 + sdel[t], 0);
+  };
+  // The next group's loads: its scales and the next activation chunk, then,
+  // after an ordering fence, its 4 weight copies.  The fence (no memory access
+  // and no instruction crosses it) makes those 4 copies the only loads issued
+  // after the activation chunk's, whatever the compiler drops (the scales of
+  // a group past the end are never used) or reorders before it.
+  auto prefetch_group = [&](int st, int g, int ch) {
+    prefetch_scales(g);
+    prefetch_a(1, ch);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch_b(st, g);
   };
 
   const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t dq_magic = 0x64006400u;
   asm volatile("" : "+v"(dq_magic));
 
-  constexpr int PS_DQ_VALU = BF ? 22 : 17;  // VALU instructions per dequantised fragment
   f32x16_t acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -710,16 +736,15 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
 
   // Copies in flight: the next activation chunk, and the weights and scales
   // of the next group from the first chunk of a group on (two chunks ahead).
-  // Each wave issues 4 copies per activation chunk and 4 copies + NT scale
-  // loads per group, so a chunk's own copies have landed when none (first
-  // chunk of a group) or 4 + NT (second) of the wave's later loads are
-  // outstanding.
+  // A chunk's own copies have landed when none (first chunk of a group) or
+  // only the next group's 4 weight copies (second chunk, issued after its
+  // copies) of the wave's loads are outstanding.
   PsScale sc[NT];
   auto start_chunk = [&](int half) {
     if (half == 0)
       asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
     else
-      asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)" ::: "memory");
+      asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)" ::: "memory");
     if (half == 0) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) sc[t] = ps_scale<BF>(sc_raw[t]);
@@ -727,7 +752,6 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  static_assert(NT == 2, "the wait count above assumes 4 + NT = 6");
 
   // One 64-k chunk: activation stage AS, weight stage BS, half HF of the group.
 #define EXQ_PS_CHUNK(AS, BS, HF, PF)                                                         \
@@ -737,13 +761,12 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
     uint4 bw[NT];                                                                            \
     _Pragma("unroll") for (int t = 0; t < NT; ++t)                                           \
         bw[t] = *reinterpret_cast<const uint4*>(                                             \
-            B_ + ((boff + ps_brow<MODE>(wn, t) * 64) ^ (32 * HF)));                          \
+            B_ + ((boff + ps_brow<MODE, TN>(wn, t) * 64) ^ (32 * HF)));                      \
     uint4 af[2][MT], wf[2][NT];                                                              \
     _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                        \
         af[0][mt] = *reinterpret_cast<const uint4*>(A_ + aoff + mt * 32 * 128);              \
     _Pragma("unroll") for (int t = 0; t < NT; ++t)                                           \
         wf[0][t] = deq_scaled<BF>(bw[t].x, sc[t], dq_mask, dq_magic);                        \
-    __builtin_amdgcn_sched_barrier(0);                                                       \
     _Pragma("unroll") for (int s = 0; s < 4; ++s) {                                          \
       const int c_ = s & 1, n_ = c_ ^ 1;                                                     \
       if (s < 3) {                                                                           \
@@ -758,12 +781,7 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
       _Pragma("unroll") for (int mt = 0; mt < MT; ++mt)                                      \
           _Pragma("unroll") for (int t = 0; t < NT; ++t)                                     \
               acc[mt][t] = mfma32<BF>(af[c_][mt], wf[c_][t], acc[mt][t]);                    \
-      if (s == 0) {                                                                          \
-        PF;                                                                                  \
-        tile_interleave_hint_vm<MT * NT, MT, PS_DQ_VALU * NT, HF ? 4 : 8 + NT>();             \
-      } else if (s < 3) {                                                                    \
-        tile_interleave_hint<MT * NT, MT, PS_DQ_VALU * NT>();                                 \
-      }                                                                                      \
+      if (s == 0) { PF; }                                                                    \
       __builtin_amdgcn_sched_barrier(0);                                                     \
     }                                                                                        \
   } while (0)
@@ -775,10 +793,11 @@ __global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta)
 #define EXQ_PS_GROUP(G, BS)                                                                  \
   do {                                                                                       \
     start_chunk(0);                                                                          \
-    EXQ_PS_CHUNK(0, BS, 0, (prefetch_a(1, 2 * (G) + 1), prefetch_b((BS) ^ 1, (G) + 1)));     \
+    EXQ_PS_CHUNK(0, BS, 0, prefetch_group((BS) ^ 1, (G) + 1, 2 * (G) + 1));                  \
     start_chunk(1);                                                                          \
     EXQ_PS_CHUNK(1, BS, 1, prefetch_a(0, 2 * (G) + 2));                                      \
   } while (0)
+  prefetch_scales(0);
   prefetch_a(0, 0);
   prefetch_b(0, 0);
   int g = 0;
