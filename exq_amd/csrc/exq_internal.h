@@ -84,6 +84,10 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
                      int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s,
                      int shape = TILE_128x128);
+// The INT4 tiles of a 256-row shape and the BF16 tiles of one projection in one
+// launch (INT4 units first): the BF16 units fill the INT4 grid's last round.
+int launch_tile_pair(int mode, bool bf, int shape, const GemmArgs& a, const float* rs,
+                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s);
 
 // INT4 grouped GEMMs for the shapes outside the tiled / grouped kernels
 // (general.hip): K % 32 == 0, a group size that is a multiple of 32 dividing

@@ -695,6 +695,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
                                             : (b13.i8 != nullptr || (has_i4 && !tile) ||
                                                (has_bf && !tile_bf));
     const bool run_tile = tile && has_i4, run_tile_bf = tile_bf && has_bf;
+    // INT4 tiles 256 rows wide and BF16 tiles: one launch per projection
+    const bool pair = run_tile && run_tile_bf && shape != TILE_128x128;
     float* rs = reinterpret_cast<float*>(ws + L.rs);
     // gate/up + SiLU: x = hidden, K = H, rows = 2I, out = mid [n, I] (sorted rows)
     g.n_blocks = I / 16;
@@ -709,7 +711,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
-    if (run_tile_bf) {
+    if (run_tile_bf && !pair) {
       st = launch_tile_gemm(0, MODE_GATEUP, bf, g, nullptr, 0, (int64_t)T * H * 2, L.tg_cap, s);
       if (st) return st;
     }
@@ -718,7 +720,9 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
         st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
         if (st) return st;
       }
-      st = launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s, shape);
+      st = pair ? launch_tile_pair(MODE_GATEUP, bf, shape, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s)
+                : launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s,
+                                   shape);
       if (st) return st;
     }
     st = record_stage(2, s);
@@ -737,7 +741,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
-    if (run_tile_bf) {
+    if (run_tile_bf && !pair) {
       st = launch_tile_gemm(0, MODE_DOWN, bf, g, nullptr, 0, 0, L.tg_cap, s);
       if (st) return st;
     }
@@ -746,7 +750,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
         st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
         if (st) return st;
       }
-      st = launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s, shape);
+      st = pair ? launch_tile_pair(MODE_DOWN, bf, shape, g, rs, L.n, 0, L.tg_cap, s)
+                : launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s, shape);
       if (st) return st;
     }
   }

@@ -159,12 +159,12 @@ struct TileArgs {
 // XCD takes a contiguous range of units; inside it, 64 consecutive units are
 // 8 token groups x 8 weight tiles, so concurrently running tiles share
 // activation and weight chunks in that XCD's L2.  False: no unit.
-__device__ __forceinline__ bool tile_unit(const GemmArgs& a, int t0, int n, int NT, TgEntry& te,
-                                          int& nt) {
+__device__ __forceinline__ bool tile_unit(const GemmArgs& a, int t0, int n, int NT, int bid,
+                                          TgEntry& te, int& nt) {
   const int U = ((n + 7) >> 3) * 8 * NT;
   const int per = (U + 7) >> 3;
-  const int local = blockIdx.x >> 3;
-  const int v = (blockIdx.x & 7) * per + local;
+  const int local = bid >> 3;
+  const int v = (bid & 7) * per + local;
   if (local >= per || v >= U) return false;
   const int tb = v / (8 * NT);
   const int rem = v - tb * 8 * NT;
@@ -298,23 +298,26 @@ __device__ __forceinline__ void tile_scale_hint() {
 //   MT = 4, NTW = 4:  64 x 256 (the same MFMA work per chunk from 16 + 16 KiB of
 //                     copies instead of 32 + 8 KiB: activation chunks, re-read
 //                     from L2 for every weight tile, are the larger stream).
+// LDS stage sizes of the INT4 tile (activations per chunk, packed weights per chunk).
+template <int MT, int NTW>
+constexpr int tile_a_stage() { return MT * 16 * KC * 2; }
+template <int MT, int NTW>
+constexpr int tile_b_stage() { return NTW * 16 * 4 * KC / 2; }
+
+// Work-group bid of the INT4 tiles; sA* / sB* are the two stages of each operand.
 template <bool BF, int MODE, int MT, int NTW>
-__global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs ta) {
+__device__ __forceinline__ void tile_gemm_body(const GemmArgs& a, const TileArgs& ta, int bid,
+                                               unsigned char* sA0, unsigned char* sA1,
+                                               unsigned char* sB0, unsigned char* sB1) {
   constexpr int WAVES_N = 4;
   constexpr int TM = MT * 16, TN = NTW * 16 * WAVES_N;
-  constexpr int A_STAGE = TM * KC * 2;  // activations per chunk
-  constexpr int B_STAGE = TN * KC / 2;  // packed weights per chunk
   constexpr int QA = TM / 16;           // activation copies per wave and chunk (4 rows each)
   constexpr int QB = TN / 64;           // weight copies per wave and chunk (16 rows each)
   constexpr int RSR = MT / 4;           // row sums held per lane (64 rows each)
-  __shared__ __attribute__((aligned(1024))) unsigned char sA0[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sA1[A_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sB0[B_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sB1[B_STAGE];
 
   TgEntry te;
   int nt;
-  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, te, nt)) return;  // INT4 groups
+  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, bid, te, nt)) return;  // INT4 groups
   const int cnt = te.cnt, pos0 = te.pos0;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -615,20 +618,19 @@ __device__ __forceinline__ int ps_brow(int wn, int t) {
 // one work-group per CU, each activation chunk feeding 512 weight rows,
 // measured 8 % slower for Mixtral: every chunk's barrier then holds all the
 // CU's waves.)
+constexpr int PS_B_STAGE = TT * PS_B_ROW;     // weight rows of the tile x one group
+
 template <bool BF, int MODE>
-__global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta) {
+__device__ __forceinline__ void tile_ps_body(const GemmArgs& a, const TileArgs& ta, int bid,
+                                             unsigned char* sA0, unsigned char* sA1,
+                                             unsigned char* sB0, unsigned char* sB1) {
   constexpr int W = TT / 64;
   constexpr int MT = 4, NT = 2, TN = 64 * W;
   constexpr int QA = 16 / W;                    // activation copies per wave and chunk
-  constexpr int PS_B_STAGE = TN * PS_B_ROW;     // 4 weight copies per wave and group
-  __shared__ __attribute__((aligned(1024))) unsigned char sA0[PS_A_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sA1[PS_A_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sB0[PS_B_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sB1[PS_B_STAGE];
 
   TgEntry te;
   int nt;
-  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, te, nt)) return;  // INT4 groups
+  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, bid, te, nt)) return;  // INT4 groups
   const int cnt = te.cnt, pos0 = te.pos0;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -851,16 +853,14 @@ constexpr int AB_STAGE = 128 * KCB * 2;  // 16 KiB per operand and stage
 __device__ __forceinline__ int bf_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
 template <bool BF, int MODE>
-__global__ void __launch_bounds__(TT, 2) tile_gemm_bf16_kernel(GemmArgs a, TileArgs ta) {
+__device__ __forceinline__ void tile_gemm_bf16_body(const GemmArgs& a, const TileArgs& ta, int bid,
+                                                    unsigned char* sA0, unsigned char* sA1,
+                                                    unsigned char* sB0, unsigned char* sB1) {
   constexpr int MT = 4, NTW = 4, WAVES_N = 2;
-  __shared__ __attribute__((aligned(1024))) unsigned char sA0[AB_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sA1[AB_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sB0[AB_STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char sB1[AB_STAGE];
 
   TgEntry te;
   int nt;
-  if (!tile_unit(a, 0, a.hdr[2], ta.n_tiles, te, nt)) return;  // BF16 groups
+  if (!tile_unit(a, 0, a.hdr[2], ta.n_tiles, bid, te, nt)) return;  // BF16 groups
   const int cnt = te.cnt, pos0 = te.pos0;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -989,6 +989,64 @@ __global__ void __launch_bounds__(256) group_rowsum_kernel(const uint16_t* __res
   }
 }
 
+// ---- kernels ------------------------------------------------------------------
+// Each stage array is its own LDS object, so the compiler can tell that reading
+// one stage cannot touch another's pending copy.
+template <bool BF, int MODE, int MT, int NTW>
+__global__ void __launch_bounds__(TT, 2) tile_gemm_kernel(GemmArgs a, TileArgs ta) {
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[tile_a_stage<MT, NTW>()];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[tile_a_stage<MT, NTW>()];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[tile_b_stage<MT, NTW>()];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[tile_b_stage<MT, NTW>()];
+  tile_gemm_body<BF, MODE, MT, NTW>(a, ta, blockIdx.x, sA0, sA1, sB0, sB1);
+}
+
+template <bool BF, int MODE>
+__global__ void __launch_bounds__(TT, 2) tile_ps_kernel(GemmArgs a, TileArgs ta) {
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[PS_A_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[PS_A_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[PS_B_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[PS_B_STAGE];
+  tile_ps_body<BF, MODE>(a, ta, blockIdx.x, sA0, sA1, sB0, sB1);
+}
+
+template <bool BF, int MODE>
+__global__ void __launch_bounds__(TT, 2) tile_gemm_bf16_kernel(GemmArgs a, TileArgs ta) {
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[AB_STAGE];
+  tile_gemm_bf16_body<BF, MODE>(a, ta, blockIdx.x, sA0, sA1, sB0, sB1);
+}
+
+// The INT4 tiles (64 x 256 or 128 x 256 scaled-operand) and the BF16 tiles of
+// one projection in one grid: work-groups [0, n_i4) run INT4 units, the rest
+// BF16 units.  Both take 16 KiB per operand stage, so the LDS is shared.  The
+// longer INT4 units are dispatched first and the BF16 units fill the INT4
+// grid's last, partly empty round (run back to back, each launch ends with
+// one: DeepSeek-V2-Lite's INT4 gate/up at 2048 tokens is 7.05 rounds of the
+// 512 resident work-groups).
+template <bool BF, int MODE, int SHAPE>
+__global__ void __launch_bounds__(TT, 2) tile_pair_kernel(GemmArgs a, TileArgs ti4, TileArgs tbf,
+                                                          int n_i4) {
+  static_assert(tile_a_stage<4, 4>() == AB_STAGE && tile_b_stage<4, 4>() == AB_STAGE &&
+                    PS_A_STAGE == AB_STAGE && PS_B_STAGE == AB_STAGE,
+                "one LDS layout for both tiles");
+  __shared__ __attribute__((aligned(1024))) unsigned char sA0[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sA1[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB0[AB_STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char sB1[AB_STAGE];
+  const int bid = (int)blockIdx.x;
+  if (bid < n_i4) {
+    if constexpr (SHAPE == TILE_PS_128x256)
+      tile_ps_body<BF, MODE>(a, ti4, bid, sA0, sA1, sB0, sB1);
+    else
+      tile_gemm_body<BF, MODE, 4, 4>(a, ti4, bid, sA0, sA1, sB0, sB1);
+  } else {
+    tile_gemm_bf16_body<BF, MODE>(a, tbf, bid - n_i4, sA0, sA1, sB0, sB1);
+  }
+}
+
 }  // namespace
 
 bool tile_gemm_applies(int tier, int mode, int n_rows, int inter, int K, int group_size) {
@@ -1073,6 +1131,45 @@ int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float
   if (mode == MODE_GATEUP) return launch_tile_mode<MODE_GATEUP>(tier, bf, shape, a, t, grid, s);
   if (mode == MODE_DOWN) return launch_tile_mode<MODE_DOWN>(tier, bf, shape, a, t, grid, s);
   return launch_tile_mode<MODE_PLAIN>(tier, bf, shape, a, t, grid, s);
+}
+
+template <int MODE, int SHAPE>
+static int launch_pair_mode(bool bf, const GemmArgs& a, const TileArgs& ti4, const TileArgs& tbf,
+                            int n_i4, int64_t grid, hipStream_t s) {
+  const dim3 g((unsigned)grid), b(TT);
+  if (bf)
+    hipLaunchKernelGGL((tile_pair_kernel<true, MODE, SHAPE>), g, b, 0, s, a, ti4, tbf, n_i4);
+  else
+    hipLaunchKernelGGL((tile_pair_kernel<false, MODE, SHAPE>), g, b, 0, s, a, ti4, tbf, n_i4);
+  return check_launch("tile_pair_kernel");
+}
+
+int launch_tile_pair(int mode, bool bf, int shape, const GemmArgs& a, const float* rs,
+                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s) {
+  if (shape != TILE_64x256 && shape != TILE_PS_128x256)
+    return set_error(EXQ_ERROR_UNSUPPORTED, "tile_pair: INT4 tiles must be 256 rows wide");
+  TileArgs ti4, tbf;
+  ti4.rs = rs;
+  ti4.rs_rows = (int)rs_rows;
+  ti4.x_bytes = x_bytes;
+  ti4.n_tiles = mode == MODE_GATEUP ? a.inter / 128 : a.n_rows / 256;  // 256-row INT4 tiles
+  tbf.rs = nullptr;
+  tbf.rs_rows = 0;
+  tbf.x_bytes = x_bytes;
+  tbf.n_tiles = mode == MODE_GATEUP ? a.inter / 64 : a.n_rows / 128;   // 128-row BF16 tiles
+  const int64_t per = 8 * cdiv(tg_cap, 8);
+  const int64_t n_i4 = per * ti4.n_tiles, grid = n_i4 + per * tbf.n_tiles;
+  if (grid <= 0) return EXQ_SUCCESS;
+  if (grid > INT32_MAX || rs_rows > INT32_MAX)
+    return set_error(EXQ_ERROR_UNSUPPORTED, "tile_pair: problem too large");
+  const bool ps = shape == TILE_PS_128x256;
+  if (mode == MODE_GATEUP)
+    return ps ? launch_pair_mode<MODE_GATEUP, TILE_PS_128x256>(bf, a, ti4, tbf, (int)n_i4, grid, s)
+              : launch_pair_mode<MODE_GATEUP, TILE_64x256>(bf, a, ti4, tbf, (int)n_i4, grid, s);
+  if (mode == MODE_DOWN)
+    return ps ? launch_pair_mode<MODE_DOWN, TILE_PS_128x256>(bf, a, ti4, tbf, (int)n_i4, grid, s)
+              : launch_pair_mode<MODE_DOWN, TILE_64x256>(bf, a, ti4, tbf, (int)n_i4, grid, s);
+  return set_error(EXQ_ERROR_UNSUPPORTED, "tile_pair: gate/up or down only");
 }
 
 }  // namespace exq
