@@ -22,7 +22,7 @@ launch (48 distinct buffers replayed from a graph: the floor at that
 transfer size) and the reference's CPU path timed on this host at every
 configuration, both variants (`cpu_baseline.configs`).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--batch 16]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 25] [--batch 16]
                     [--sweep 1,4,16,64] [--layers 48] [--no-cpu] [--no-configs]
 
 Counter runs (HBM traffic of the dominant kernel, rocprofv3 --pmc), one per
@@ -57,7 +57,9 @@ def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # 25 steps of 48 Qwen3 layers at T=16 are about 40 ms: the clocks have
+    # settled before the timed steps (WARMUP_MS)
+    ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--sweep", type=str, default="1,4,16,64")
     ap.add_argument("--layers", type=int, default=48)
@@ -185,9 +187,10 @@ def pct(v, q):
     return v[min(len(v) - 1, max(0, int(round(q / 100.0 * (len(v) - 1)))))]
 
 
-def time_steps(stack, b, steps, warmup, use_graph):
+def time_steps(stack, b, steps, warmup, use_graph, warmup_ms=0.0):
     """Returns (ms per step over the bracketed K steps, host wall ms per step,
-    list of per-step ms from events recorded between the steps)."""
+    list of per-step ms from events recorded between the steps), after
+    `warmup` untimed steps (or at least warmup_ms of them)."""
     import torch
     if use_graph:
         s = torch.cuda.Stream()
@@ -202,7 +205,7 @@ def time_steps(stack, b, steps, warmup, use_graph):
         fn = g.replay
     else:
         fn = lambda: run_step(stack, b)  # noqa: E731
-    for _ in range(warmup):
+    for _ in range(_warmup_count(fn, warmup, warmup_ms)):
         fn()
     torch.cuda.synchronize()
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
@@ -259,9 +262,31 @@ def stage_times(layers, b, reps=7):
 MFMA_PEAK_BF16_TFLOPS = 2500.0
 
 
-def _graph_times(fn, reps, warmup=3):
+# Untimed work before a timed series of a configuration: after an idle spell
+# the first ~10-15 ms of back-to-back work run slower while the clocks settle
+# (measured from a cold start: Qwen3 T=1 15.2 -> 13.4 us per layer over the
+# first 15 steps of 48 layers, T=16 35.8 -> 33.2 over 11; DeepSeek-V2-Lite
+# prefill 519 -> 450 us over the first 20 replays).
+WARMUP_MS = 40.0
+
+
+def _warmup_count(replay, minimum, warmup_ms):
+    """Replays of `replay` (already warm once) that make up warmup_ms."""
+    import torch
+    if warmup_ms <= 0:
+        return minimum
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return max(minimum, int(warmup_ms / max(e0.elapsed_time(e1), 1e-3)) + 1)
+
+
+def _graph_times(fn, reps, warmup=3, warmup_ms=0.0):
     """Per-replay ms of `fn` captured once in a HIP graph and replayed `reps`
-    times (events recorded between the replays)."""
+    times (events recorded between the replays), after `warmup` replays or
+    at least warmup_ms of them."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -272,7 +297,7 @@ def _graph_times(fn, reps, warmup=3):
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         fn()
-    for _ in range(warmup):
+    for _ in range(_warmup_count(g.replay, warmup, warmup_ms)):
         g.replay()
     torch.cuda.synchronize()
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
@@ -336,14 +361,19 @@ def _prefill_call(dev, name, weights=None):
 
 
 def prefill_rows(calls, reps):
+    """µs per layer (P50 over `reps` graph replays, P5 / P95 beside it) of each
+    prefill call, after WARMUP_MS of untimed replays."""
     rows = []
     for name, T, fn, flops in calls:
-        ms = _graph_time(fn, reps)
-        tf = flops / (ms * 1e-3) / 1e12
-        rows.append({"config": name, "batch": T, "us_per_layer": round(ms * 1e3, 1),
-                     "tokens_per_s": round(T / (ms * 1e-3)), "TFLOPs": round(tf, 1),
+        per = [ms * 1e3 for ms in _graph_times(fn, reps, warmup_ms=WARMUP_MS)]
+        us = pct(per, 50)
+        tf = flops / (us * 1e-6) / 1e12
+        rows.append({"config": name, "batch": T, "us_per_layer": round(us, 1),
+                     "p5_us": round(pct(per, 5), 1), "p95_us": round(pct(per, 95), 1),
+                     "replays_timed": reps, "warmup_ms": WARMUP_MS,
+                     "tokens_per_s": round(T / (us * 1e-6)), "TFLOPs": round(tf, 1),
                      "frac_of_mfma_peak": round(tf / MFMA_PEAK_BF16_TFLOPS, 4)})
-        log(f"config {name} prefill T={T}: {ms * 1e3:.1f} us/layer, {tf:.1f} TFLOP/s")
+        log(f"config {name} prefill T={T}: {us:.1f} us/layer P50, {tf:.1f} TFLOP/s")
     return rows
 
 
@@ -388,7 +418,8 @@ def measure_configs(dev, reps, cpu=None, north_star_only=False):
         # replays (>= 300 layer calls).
         seq = calls * max(1, -(-48 // len(calls)))
         n_rep = max(reps, -(-300 // len(seq)))
-        per = [ms * 1e3 / len(seq) for ms in _graph_times(lambda: [c() for c in seq], n_rep)]
+        per = [ms * 1e3 / len(seq)
+               for ms in _graph_times(lambda: [c() for c in seq], n_rep, warmup_ms=WARMUP_MS)]
         us = pct(per, 50)
         gbps = bytes_per_call / (us * 1e-6) / 1e9
         rows.append({"config": name, "batch": T, "layers_rotated": n_layers,
@@ -534,7 +565,7 @@ def measure_configs(dev, reps, cpu=None, north_star_only=False):
         decode_row("deepseek_v2_lite", cfg, T, calls, nbytes / len(banks), len(banks))
         if T != 16:
             cpu_bank("deepseek_v2_lite", T, x, banks[0], rts[0][0], rts[0][1])
-    rows += prefill_rows([_prefill_call(dev, "deepseek_v2_lite", banks[0])], max(3, reps // 10))
+    rows += prefill_rows([_prefill_call(dev, "deepseek_v2_lite", banks[0])], max(20, reps))
     del banks
     torch.cuda.empty_cache()
 
@@ -554,7 +585,7 @@ def measure_configs(dev, reps, cpu=None, north_star_only=False):
                          fused_experts(x, p13, s13, p2, s2, tw, tid, workspace=ws))
         decode_row("mixtral", cfg, T, calls, nbytes / len(layers), len(layers))
         cpu_int4("mixtral", T, x, layers[0], rts[0][0], rts[0][1])
-    rows += prefill_rows([_prefill_call(dev, "mixtral", layers[0])], max(3, reps // 10))
+    rows += prefill_rows([_prefill_call(dev, "mixtral", layers[0])], max(20, reps))
     del layers
     torch.cuda.empty_cache()
 
@@ -816,7 +847,7 @@ def main():
                 torch.cuda.synchronize()
                 log(f"{name} prefill: one eager call")
             else:
-                rows += prefill_rows([call], max(3, args.steps // 10))
+                rows += prefill_rows([call], max(20, args.steps))
             del call
             torch.cuda.empty_cache()
         if rows:
@@ -868,7 +899,8 @@ def main():
     sweep = []
     for T in [int(v) for v in args.sweep.split(",") if v.strip()]:
         bb = b if T == args.batch else Batch(stack, T, dev)
-        _, _, pr = time_steps(stack, bb, max(10, args.steps // 2), args.warmup, use_graph)
+        _, _, pr = time_steps(stack, bb, max(10, args.steps // 2), args.warmup, use_graph,
+                              warmup_ms=WARMUP_MS)
         pl = [m * 1e3 / args.layers for m in pr]
         ul = pct(pl, 50)
         g = bb.bytes / (ul * args.layers * 1e-6) / 1e9

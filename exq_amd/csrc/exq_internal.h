@@ -11,6 +11,9 @@ namespace exq {
 // of the prefill kernels, eight on the 128 x 128 tiles.
 constexpr int kTokenGroup = 64;
 constexpr int kTokenGroupI4 = 128;
+// On the 64 x 256 INT4 prefill tiles, an INT4 expert with at least this many
+// routed rows takes 128-row token groups on the 128 x 256 scaled-operand tiles.
+constexpr int kI4BigMinRows = 384;
 
 // One work item of the grouped kernels: rows [pos0, pos0 + cnt) of the
 // expert-sorted order, all routed to expert `e` whose precision tier is
@@ -44,7 +47,8 @@ struct Bank {
 };
 
 struct GemmArgs {
-  const int* hdr;          // [0] token groups, [1] first INT4 group, [2] first INT8 group
+  const int* hdr;          // [0] token groups, [1] first INT4 group, [2] first INT8 group,
+                           // [3] first INT4 group of the small-group experts
   const TgEntry* tg;
   int n_blocks;            // row blocks per token group
   const uint16_t* x;       // activations (f16/bf16 bits)
@@ -84,10 +88,15 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
                      int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s,
                      int shape = TILE_128x128);
-// The INT4 tiles of a 256-row shape and the BF16 tiles of one projection in one
-// launch (INT4 units first): the BF16 units fill the INT4 grid's last round.
-int launch_tile_pair(int mode, bool bf, int shape, const GemmArgs& a, const float* rs,
-                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s);
+// The tiles of one projection in one launch (tile_mix_kernel): 128 x 256
+// scaled-operand INT4 tiles over token groups [hdr[1], hdr[3]), 64 x 256 INT4
+// tiles over [hdr[3], hdr[0]) (row sums from launch_group_rowsum), then BF16
+// tiles over [0, hdr[2]).  cap_* bound each range's token groups (0: the range
+// is empty); the grid is sized from them and each range's real size is read
+// on the device.
+int launch_tile_mix(int mode, bool bf, const GemmArgs& a, const float* rs, int64_t rs_rows,
+                    int64_t x_bytes, int64_t cap_ps, int64_t cap_64, int64_t cap_bf,
+                    hipStream_t s);
 
 // INT4 grouped GEMMs for the shapes outside the tiled / grouped kernels
 // (general.hip): K % 32 == 0, a group size that is a multiple of 32 dividing
@@ -103,13 +112,19 @@ struct RoutePlanParams {
   int T, k, kp, E, Ep;  // kp = k + n_shared, Ep = E + n_shared
   int n;                // T * kp
   const int8_t* tier;   // [Ep] or null (all INT4)
-  int* hdr;             // [0] token groups, [1] first INT4 group, [2] first INT8 group
+  int* hdr;             // [0] token groups, [1] first INT4 group, [2] first INT8 group,
+                        // [3] first INT4 group of an expert below i4_big_rows
   int* ends;            // [Ep + 1]
   int* sorted;          // [n] slot ids in expert-sorted order
   TgEntry* tg;          // [tg_cap]
   int tg_cap;
   int i4_group;         // rows per INT4 token group (kTokenGroup or kTokenGroupI4)
   int bf_group;         // rows per BF16 token group (kTokenGroup or kTokenGroupI4)
+  // INT4 experts with at least i4_big_rows routed rows (none when 0) take
+  // groups of i4_big_group rows and are listed before the other INT4 experts;
+  // hdr[3] = the first group of those others (hdr[0] when there are none)
+  int i4_big_rows;
+  int i4_big_group;
   int* counters;        // combine arrival counters, zeroed here
   int n_counters;
   int64_t* sort_order_out;  // optional [T*k]

@@ -589,9 +589,18 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
   // Otherwise 128 x 128.
   const bool wide_ok = tile && tile_gemm_wide_applies(MODE_GATEUP, 2 * I, I) &&
                        tile_gemm_wide_applies(MODE_DOWN, H, I);
+  // With the 64 x 256 tiles, the INT4 experts that received at least
+  // kI4BigMinRows rows take the 128 x 256 scaled-operand tiles in the same
+  // launch (128-row token groups listed first): a skewed router leaves a few
+  // experts with most of the rows (DeepSeek-V2-Lite at 2048 tokens: 8 of 64
+  // experts hold 72 % of the routed rows).  An expert has at most T rows
+  // unless a token repeats an id, so smaller batches keep one shape.
   const int shape = !wide_ok ? TILE_128x128
                              : ((int64_t)T * k < 512 * (int64_t)E ? TILE_64x256 : TILE_PS_128x256);
-  rp.i4_group = tile ? (shape == TILE_64x256 ? kTokenGroup : kTokenGroupI4) : kTokenGroup;
+  const bool i4_mixed = shape == TILE_64x256 && T >= kI4BigMinRows;
+  rp.i4_group = tile && shape != TILE_64x256 ? kTokenGroupI4 : kTokenGroup;
+  rp.i4_big_rows = !tile ? 0 : (shape == TILE_PS_128x256 ? 1 : (i4_mixed ? kI4BigMinRows : 0));
+  rp.i4_big_group = kTokenGroupI4;
   rp.bf_group = tile_bf ? kTokenGroupI4 : kTokenGroup;
   rp.counters = nullptr;
   rp.n_counters = 0;
@@ -695,8 +704,16 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
                                             : (b13.i8 != nullptr || (has_i4 && !tile) ||
                                                (has_bf && !tile_bf));
     const bool run_tile = tile && has_i4, run_tile_bf = tile_bf && has_bf;
-    // INT4 tiles 256 rows wide and BF16 tiles: one launch per projection
-    const bool pair = run_tile && run_tile_bf && shape != TILE_128x128;
+    // INT4 tiles 256 rows wide of both shapes, and BF16 tiles: one launch per
+    // projection (tile_mix_kernel), each range bounded by cap_*
+    const bool mix = run_tile && shape != TILE_128x128 && (run_tile_bf || i4_mixed);
+    const int64_t cap_ps =
+        shape == TILE_PS_128x256
+            ? L.tg_cap
+            : (i4_mixed ? std::min<int64_t>(L.tg_cap, cdiv(L.n, kTokenGroupI4) + L.n / kI4BigMinRows)
+                        : 0);
+    const int64_t cap_64 = shape == TILE_64x256 ? L.tg_cap : 0;
+    const int64_t cap_bf = run_tile_bf ? L.tg_cap : 0;
     float* rs = reinterpret_cast<float*>(ws + L.rs);
     // gate/up + SiLU: x = hidden, K = H, rows = 2I, out = mid [n, I] (sorted rows)
     g.n_blocks = I / 16;
@@ -711,7 +728,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_GATEUP>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
-    if (run_tile_bf && !pair) {
+    if (run_tile_bf && !mix) {
       st = launch_tile_gemm(0, MODE_GATEUP, bf, g, nullptr, 0, (int64_t)T * H * 2, L.tg_cap, s);
       if (st) return st;
     }
@@ -720,9 +737,10 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
         st = launch_group_rowsum(bf, g.x, H, T, H, gs, rs, s);
         if (st) return st;
       }
-      st = pair ? launch_tile_pair(MODE_GATEUP, bf, shape, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s)
-                : launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s,
-                                   shape);
+      st = mix ? launch_tile_mix(MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, cap_ps, cap_64,
+                                 cap_bf, s)
+               : launch_tile_gemm(2, MODE_GATEUP, bf, g, rs, T, (int64_t)T * H * 2, L.tg_cap, s,
+                                  shape);
       if (st) return st;
     }
     st = record_stage(2, s);
@@ -741,7 +759,7 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       st = launch_gemm<MODE_DOWN>(bf, g, L.tg_cap * g.n_blocks, s);
       if (st) return st;
     }
-    if (run_tile_bf && !pair) {
+    if (run_tile_bf && !mix) {
       st = launch_tile_gemm(0, MODE_DOWN, bf, g, nullptr, 0, 0, L.tg_cap, s);
       if (st) return st;
     }
@@ -750,8 +768,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
         st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
         if (st) return st;
       }
-      st = pair ? launch_tile_pair(MODE_DOWN, bf, shape, g, rs, L.n, 0, L.tg_cap, s)
-                : launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s, shape);
+      st = mix ? launch_tile_mix(MODE_DOWN, bf, g, rs, L.n, 0, cap_ps, cap_64, cap_bf, s)
+               : launch_tile_gemm(2, MODE_DOWN, bf, g, rs, L.n, 0, L.tg_cap, s, shape);
       if (st) return st;
     }
   }

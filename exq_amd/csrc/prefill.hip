@@ -150,6 +150,7 @@ struct TileArgs {
   int rs_rows;
   int64_t x_bytes;   // bytes addressable from a.x (GATEUP gather)
   int n_tiles;       // weight tiles per expert (I / (TN / 2) for GATEUP, rows / TN otherwise)
+  int h_lo, h_hi;    // INT4 tiles: token groups [hdr[h_lo], hdr[h_hi]) of the list
 };
 
 // ---- shared pieces of the tiled kernels --------------------------------------
@@ -317,7 +318,8 @@ __device__ __forceinline__ void tile_gemm_body(const GemmArgs& a, const TileArgs
 
   TgEntry te;
   int nt;
-  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, bid, te, nt)) return;  // INT4 groups
+  if (!tile_unit(a, a.hdr[ta.h_lo], a.hdr[ta.h_hi] - a.hdr[ta.h_lo], ta.n_tiles, bid, te, nt))
+    return;  // INT4 groups [hdr[h_lo], hdr[h_hi])
   const int cnt = te.cnt, pos0 = te.pos0;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -630,7 +632,8 @@ __device__ __forceinline__ void tile_ps_body(const GemmArgs& a, const TileArgs& 
 
   TgEntry te;
   int nt;
-  if (!tile_unit(a, a.hdr[1], a.hdr[0] - a.hdr[1], ta.n_tiles, bid, te, nt)) return;  // INT4 groups
+  if (!tile_unit(a, a.hdr[ta.h_lo], a.hdr[ta.h_hi] - a.hdr[ta.h_lo], ta.n_tiles, bid, te, nt))
+    return;  // INT4 groups [hdr[h_lo], hdr[h_hi])
   const int cnt = te.cnt, pos0 = te.pos0;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1019,32 +1022,46 @@ __global__ void __launch_bounds__(TT, 2) tile_gemm_bf16_kernel(GemmArgs a, TileA
   tile_gemm_bf16_body<BF, MODE>(a, ta, blockIdx.x, sA0, sA1, sB0, sB1);
 }
 
-// The INT4 tiles (64 x 256 or 128 x 256 scaled-operand) and the BF16 tiles of
-// one projection in one grid: work-groups [0, n_i4) run INT4 units, the rest
-// BF16 units.  Both take 16 KiB per operand stage, so the LDS is shared.  The
-// longer INT4 units are dispatched first and the BF16 units fill the INT4
-// grid's last, partly empty round (run back to back, each launch ends with
-// one: DeepSeek-V2-Lite's INT4 gate/up at 2048 tokens is 7.05 rounds of the
-// 512 resident work-groups).
-template <bool BF, int MODE, int SHAPE>
-__global__ void __launch_bounds__(TT, 2) tile_pair_kernel(GemmArgs a, TileArgs ti4, TileArgs tbf,
-                                                          int n_i4) {
+// Work-groups of tile_unit's unit range over n token groups (a multiple of
+// eight groups times the weight tiles per group).
+__device__ __forceinline__ int tile_unit_count(int n, int n_tiles) {
+  return ((n + 7) >> 3) * 8 * n_tiles;
+}
+
+// The tiles of one projection in one grid, in three ranges whose sizes come
+// from the token-group list on the device: 128 x 256 scaled-operand INT4 tiles
+// over the big-group INT4 experts [hdr[1], hdr[3]), 64 x 256 INT4 tiles over
+// the other INT4 experts [hdr[3], hdr[0]), then BF16 tiles over [0, hdr[2]).
+// All three take 16 KiB per operand stage, so the LDS is shared.  The host
+// sizes the grid from upper bounds; the work-groups past the three ranges
+// return at once, after every real unit in dispatch order.  The longest units
+// (the big experts' 128-row tiles) go first and the BF16 units fill the last,
+// partly empty round of the INT4 ones (DeepSeek-V2-Lite's INT4 gate/up at
+// 2048 tokens is several rounds of the 512 resident work-groups).
+template <bool BF, int MODE>
+__global__ void __launch_bounds__(TT, 2) tile_mix_kernel(GemmArgs a, TileArgs tps, TileArgs t64,
+                                                         TileArgs tbf) {
   static_assert(tile_a_stage<4, 4>() == AB_STAGE && tile_b_stage<4, 4>() == AB_STAGE &&
                     PS_A_STAGE == AB_STAGE && PS_B_STAGE == AB_STAGE,
-                "one LDS layout for both tiles");
+                "one LDS layout for the three tiles");
   __shared__ __attribute__((aligned(1024))) unsigned char sA0[AB_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sA1[AB_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sB0[AB_STAGE];
   __shared__ __attribute__((aligned(1024))) unsigned char sB1[AB_STAGE];
-  const int bid = (int)blockIdx.x;
-  if (bid < n_i4) {
-    if constexpr (SHAPE == TILE_PS_128x256)
-      tile_ps_body<BF, MODE>(a, ti4, bid, sA0, sA1, sB0, sB1);
-    else
-      tile_gemm_body<BF, MODE, 4, 4>(a, ti4, bid, sA0, sA1, sB0, sB1);
-  } else {
-    tile_gemm_bf16_body<BF, MODE>(a, tbf, bid - n_i4, sA0, sA1, sB0, sB1);
+  int bid = (int)blockIdx.x;
+  const int u_ps = tile_unit_count(a.hdr[3] - a.hdr[1], tps.n_tiles);
+  if (bid < u_ps) {
+    tile_ps_body<BF, MODE>(a, tps, bid, sA0, sA1, sB0, sB1);
+    return;
   }
+  bid -= u_ps;
+  const int u_64 = tile_unit_count(a.hdr[0] - a.hdr[3], t64.n_tiles);
+  if (bid < u_64) {
+    tile_gemm_body<BF, MODE, 4, 4>(a, t64, bid, sA0, sA1, sB0, sB1);
+    return;
+  }
+  bid -= u_64;
+  if (tbf.n_tiles > 0) tile_gemm_bf16_body<BF, MODE>(a, tbf, bid, sA0, sA1, sB0, sB1);
 }
 
 }  // namespace
@@ -1121,6 +1138,8 @@ int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float
   t.rs = rs;
   t.rs_rows = (int)rs_rows;
   t.x_bytes = x_bytes;
+  t.h_lo = 1;  // every INT4 group (one tile shape)
+  t.h_hi = 0;
   if (tier != 2) shape = TILE_128x128;
   const int tn = shape == TILE_128x128 ? 128 : 256;
   t.n_tiles = mode == MODE_GATEUP ? a.inter / (tn / 2) : a.n_rows / tn;
@@ -1133,43 +1152,47 @@ int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float
   return launch_tile_mode<MODE_PLAIN>(tier, bf, shape, a, t, grid, s);
 }
 
-template <int MODE, int SHAPE>
-static int launch_pair_mode(bool bf, const GemmArgs& a, const TileArgs& ti4, const TileArgs& tbf,
-                            int n_i4, int64_t grid, hipStream_t s) {
+template <int MODE>
+static int launch_mix_mode(bool bf, const GemmArgs& a, const TileArgs& tps, const TileArgs& t64,
+                           const TileArgs& tbf, int64_t grid, hipStream_t s) {
   const dim3 g((unsigned)grid), b(TT);
   if (bf)
-    hipLaunchKernelGGL((tile_pair_kernel<true, MODE, SHAPE>), g, b, 0, s, a, ti4, tbf, n_i4);
+    hipLaunchKernelGGL((tile_mix_kernel<true, MODE>), g, b, 0, s, a, tps, t64, tbf);
   else
-    hipLaunchKernelGGL((tile_pair_kernel<false, MODE, SHAPE>), g, b, 0, s, a, ti4, tbf, n_i4);
-  return check_launch("tile_pair_kernel");
+    hipLaunchKernelGGL((tile_mix_kernel<false, MODE>), g, b, 0, s, a, tps, t64, tbf);
+  return check_launch("tile_mix_kernel");
 }
 
-int launch_tile_pair(int mode, bool bf, int shape, const GemmArgs& a, const float* rs,
-                     int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s) {
-  if (shape != TILE_64x256 && shape != TILE_PS_128x256)
-    return set_error(EXQ_ERROR_UNSUPPORTED, "tile_pair: INT4 tiles must be 256 rows wide");
-  TileArgs ti4, tbf;
-  ti4.rs = rs;
-  ti4.rs_rows = (int)rs_rows;
-  ti4.x_bytes = x_bytes;
-  ti4.n_tiles = mode == MODE_GATEUP ? a.inter / 128 : a.n_rows / 256;  // 256-row INT4 tiles
+int launch_tile_mix(int mode, bool bf, const GemmArgs& a, const float* rs, int64_t rs_rows,
+                    int64_t x_bytes, int64_t cap_ps, int64_t cap_64, int64_t cap_bf,
+                    hipStream_t s) {
+  if (mode != MODE_GATEUP && mode != MODE_DOWN)
+    return set_error(EXQ_ERROR_UNSUPPORTED, "tile_mix: gate/up or down only");
+  TileArgs tps, t64, tbf;
+  tps.rs = nullptr;  // scaled weight operands: no row sums
+  tps.rs_rows = 0;
+  tps.x_bytes = x_bytes;
+  tps.n_tiles = mode == MODE_GATEUP ? a.inter / 128 : a.n_rows / 256;  // 256-row INT4 tiles
+  tps.h_lo = 1;
+  tps.h_hi = 3;
+  t64 = tps;
+  t64.rs = rs;
+  t64.rs_rows = (int)rs_rows;
+  t64.h_lo = 3;
+  t64.h_hi = 0;
   tbf.rs = nullptr;
   tbf.rs_rows = 0;
   tbf.x_bytes = x_bytes;
-  tbf.n_tiles = mode == MODE_GATEUP ? a.inter / 64 : a.n_rows / 128;   // 128-row BF16 tiles
-  const int64_t per = 8 * cdiv(tg_cap, 8);
-  const int64_t n_i4 = per * ti4.n_tiles, grid = n_i4 + per * tbf.n_tiles;
+  tbf.n_tiles = cap_bf > 0 ? (mode == MODE_GATEUP ? a.inter / 64 : a.n_rows / 128) : 0;
+  tbf.h_lo = 0;
+  tbf.h_hi = 2;
+  const int64_t grid = 8 * cdiv(cap_ps, 8) * tps.n_tiles + 8 * cdiv(cap_64, 8) * t64.n_tiles +
+                       8 * cdiv(cap_bf, 8) * tbf.n_tiles;
   if (grid <= 0) return EXQ_SUCCESS;
   if (grid > INT32_MAX || rs_rows > INT32_MAX)
-    return set_error(EXQ_ERROR_UNSUPPORTED, "tile_pair: problem too large");
-  const bool ps = shape == TILE_PS_128x256;
-  if (mode == MODE_GATEUP)
-    return ps ? launch_pair_mode<MODE_GATEUP, TILE_PS_128x256>(bf, a, ti4, tbf, (int)n_i4, grid, s)
-              : launch_pair_mode<MODE_GATEUP, TILE_64x256>(bf, a, ti4, tbf, (int)n_i4, grid, s);
-  if (mode == MODE_DOWN)
-    return ps ? launch_pair_mode<MODE_DOWN, TILE_PS_128x256>(bf, a, ti4, tbf, (int)n_i4, grid, s)
-              : launch_pair_mode<MODE_DOWN, TILE_64x256>(bf, a, ti4, tbf, (int)n_i4, grid, s);
-  return set_error(EXQ_ERROR_UNSUPPORTED, "tile_pair: gate/up or down only");
+    return set_error(EXQ_ERROR_UNSUPPORTED, "tile_mix: problem too large");
+  return mode == MODE_GATEUP ? launch_mix_mode<MODE_GATEUP>(bf, a, tps, t64, tbf, grid, s)
+                             : launch_mix_mode<MODE_DOWN>(bf, a, tps, t64, tbf, grid, s);
 }
 
 }  // namespace exq

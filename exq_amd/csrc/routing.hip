@@ -461,15 +461,24 @@ __device__ void plan_tail(const RoutePlanParams& p, RouteLds& s) {
   }
   const int c = b < nb ? s.cnt[b] : 0;
   const int my_tier = (b < nb) ? (p.tier ? (int)p.tier[b] : 2) : -1;
-  const int gsz = my_tier == 2 ? p.i4_group : my_tier == 0 ? p.bf_group : kTokenGroup;
+  // list class of the bucket's groups: 0 BF16, 1 INT8, 2 INT4 experts with at
+  // least i4_big_rows rows, 3 the other INT4 experts
+  const int my_cls =
+      my_tier == 2 ? (p.i4_big_rows > 0 && c >= p.i4_big_rows ? 2 : 3) : my_tier;
+  const int gsz = my_cls == 2   ? p.i4_big_group
+                  : my_cls == 3 ? p.i4_group
+                  : my_cls == 0 ? p.bf_group
+                                : kTokenGroup;
   const int ng = (c + gsz - 1) / gsz;
-  int base = 0, first_i4 = 0, first_i8 = 0;
-  for (int tr = (p.tier ? 0 : 2); tr <= 2; ++tr) {
-    if (tr == 1) first_i8 = base;
-    if (tr == 2) first_i4 = base;
+  int base = 0, first_i4 = 0, first_i8 = 0, first_i4s = 0;
+  for (int cl = (p.tier ? 0 : 2); cl <= 3; ++cl) {
+    if (cl == 1) first_i8 = base;
+    if (cl == 2) first_i4 = base;
+    if (cl == 3) first_i4s = base;
+    if (cl == 2 && p.i4_big_rows <= 0) continue;  // no big INT4 experts (uniform)
     int tot;
-    int off = block_excl_scan(my_tier == tr ? ng : 0, s.wsum, &tot);
-    if (my_tier == tr) {
+    int off = block_excl_scan(my_cls == cl ? ng : 0, s.wsum, &tot);
+    if (my_cls == cl) {
       for (int g = 0; g < ng; ++g) {
         const int slot = base + off + g;
         if (slot < p.tg_cap) {
@@ -477,7 +486,7 @@ __device__ void plan_tail(const RoutePlanParams& p, RouteLds& s) {
           te.e = b;
           te.pos0 = s.start[b] + g * gsz;
           te.cnt = min(gsz, c - g * gsz);
-          te.tier = tr;
+          te.tier = my_tier;
           p.tg[slot] = te;
         }
       }
@@ -488,6 +497,7 @@ __device__ void plan_tail(const RoutePlanParams& p, RouteLds& s) {
     p.hdr[0] = base < p.tg_cap ? base : p.tg_cap;
     p.hdr[1] = first_i4 < p.tg_cap ? first_i4 : p.tg_cap;
     p.hdr[2] = first_i8 < p.tg_cap ? first_i8 : p.tg_cap;
+    p.hdr[3] = first_i4s < p.tg_cap ? first_i4s : p.tg_cap;
   }
   for (int i = threadIdx.x; i < p.n_counters; i += RT) p.counters[i] = 0;
   if (base == 0 && p.out) {
@@ -654,6 +664,7 @@ __global__ void __launch_bounds__(RT) tg_from_ends_kernel(const int32_t* ends, i
     hdr[0] = base < tg_cap ? base : tg_cap;
     hdr[1] = tier == 2 ? 0 : hdr[0];
     hdr[2] = tier == 0 ? hdr[0] : 0;
+    hdr[3] = hdr[1];  // one group size: no big-group INT4 experts
   }
 }
 

@@ -87,6 +87,72 @@ def test_prefill_one_expert_takes_all_rows(device):
     assert_close_rel(out, ref, TOL, "prefill one expert")
 
 
+def _split_ids(T, dropped):
+    """Top-2 ids of T = 1024 tokens with row counts on both sides of the
+    per-expert tile switch (kI4BigMinRows = 384 rows): expert 0 exactly 384
+    (three full 128-row groups), expert 1 383 (six 64-row groups, the last
+    ragged), expert 2 700 (five 128-row groups + 60), expert 3 257, expert 4
+    300, experts 6-7 none, and the last 24 tokens' second ids on expert 5 or
+    dropped (-1)."""
+    ids = np.empty((T, 2), dtype=np.int64)
+    ids[:384, 0] = 0
+    ids[384:767, 0] = 1
+    ids[767:, 0] = 3
+    ids[:700, 1] = 2
+    ids[700:1000, 1] = 4
+    ids[1000:, 1] = -1 if dropped else 5
+    counts = np.bincount(ids[ids >= 0], minlength=8)
+    assert counts.tolist() == [384, 383, 700, 257, 300, 0 if dropped else 24, 0, 0]
+    return ids
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefill_per_expert_tile_shape(dtype, device):
+    """Experts averaging under 512 rows take the 64 x 256 INT4 tiles; those
+    with at least 384 rows take 128-row groups on the 128 x 256 scaled-operand
+    tiles, in the same launch.  Boundary counts 383 / 384, a ragged big
+    group and empty experts; sort order and boundaries bit-exact."""
+    from exq_amd.kernels import fused_experts
+    T, E = 1024, 8
+    banner(f"prefill per-expert tile shape {dtype}")
+    p13, s13, p2, s2 = _pack(E, 512, 1024, 980, device)
+    ids = _split_ids(T, dropped=False)
+    w = np.random.default_rng(981).random((T, 2)).astype(np.float32)
+    x = _hidden(T, 1024, 982, device, dtype)
+    so = torch.empty(T * 2, dtype=torch.int64, device=device)
+    ends = torch.empty(E + 1, dtype=torch.int32, device=device)
+    out = fused_experts(x, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                        torch.from_numpy(ids).to(device), sort_order_out=so,
+                        expert_ends_out=ends)
+    torch.cuda.synchronize()
+    r_so, r_ends, _ = routing.sort_tokens_by_expert(ids, E)
+    assert np.array_equal(so.cpu().numpy(), r_so)
+    assert np.array_equal(ends.cpu().numpy(), r_ends)
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, f"prefill per-expert tile shape {dtype}")
+
+
+@pytest.mark.parametrize("act", [torch.bfloat16, torch.float16])
+def test_prefill_per_expert_tile_shape_mixed_bank(act, device):
+    """The same split in a mixed bank: the big INT4 expert 2 and the small
+    INT4 experts 1, 3 and 4 share a launch with the BF16 experts 0 and 6
+    (expert 0 at exactly 384 rows is BF16 here); INT8 expert 5 is idle and 24
+    ids are dropped."""
+    from exq_amd.kernels import MixedExpertBank, fused_experts_mixed
+    T, E = 1024, 8
+    banner(f"prefill per-expert tile shape mixed bank {act}")
+    w13, w2 = synth.expert_weights_gpu(E, 512, 1024, 983, device)
+    bank = MixedExpertBank.from_weights(w13, w2, [0, 2, 2, 2, 2, 1, 0, 2], act_dtype=act)
+    ids = _split_ids(T, dropped=True)
+    w = np.random.default_rng(984).random((T, 2)).astype(np.float32)
+    x = _hidden(T, 1024, 985, device, act)
+    out = fused_experts_mixed(x, bank, torch.from_numpy(w).to(device),
+                              torch.from_numpy(ids).to(device))
+    from tests.test_gpu_mixed import _oracle
+    assert_close_rel(out, _oracle(bank, x, ids, w), TOL,
+                     f"prefill per-expert tile shape mixed bank {act}")
+
+
 def test_prefill_group_size_256_untiled(device):
     """group_size 256 is not tiled: the 64-row grouped kernel runs instead."""
     from exq_amd.kernels import fused_experts
