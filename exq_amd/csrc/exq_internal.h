@@ -85,6 +85,12 @@ enum TileShape { TILE_128x128 = 0, TILE_64x256 = 1, TILE_PS_128x256 = 2 };
 int64_t tile_rowsum_floats(int64_t rows, int64_t K);
 int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows, int K, int gs,
                         float* out, hipStream_t s);
+// The same sums for the expert-sorted rows of the token groups [hdr[3],
+// hdr[0]) only (the rows the 64 x 256 and 128 x 128 INT4 tiles read in the
+// down projection); cap bounds that group count, groups hold <= 128 rows.
+int launch_group_rowsum_tg(bool bf, const uint16_t* x, int64_t stride, int K, const int* hdr,
+                           const TgEntry* tg, int64_t cap, int64_t rs_rows, float* out,
+                           hipStream_t s);
 int launch_tile_gemm(int tier, int mode, bool bf, const GemmArgs& a, const float* rs,
                      int64_t rs_rows, int64_t x_bytes, int64_t tg_cap, hipStream_t s,
                      int shape = TILE_128x128);

@@ -764,8 +764,8 @@ int fused_forward_impl(const exq_moe_problem* p, const void* hidden, const void*
       if (st) return st;
     }
     if (run_tile) {
-      if (shape != TILE_PS_128x256) {
-        st = launch_group_rowsum(bf, g.x, I, L.n, I, gs, rs, s);
+      if (shape != TILE_PS_128x256) {  // sums of the rows the row-sum tiles read
+        st = launch_group_rowsum_tg(bf, g.x, I, I, rp.hdr, rp.tg, L.tg_cap, L.n, rs, s);
         if (st) return st;
       }
       st = mix ? launch_tile_mix(MODE_DOWN, bf, g, rs, L.n, 0, cap_ps, cap_64, cap_bf, s)

@@ -992,6 +992,63 @@ __global__ void __launch_bounds__(256) group_rowsum_kernel(const uint16_t* __res
   }
 }
 
+// The same sums for the expert-sorted rows of token groups [hdr[3], hdr[0])
+// only (the 64 x 256 INT4 tiles' groups; the scaled-operand and BF16 tiles
+// read none): work-group b takes rows 16 (b % 8) .. +15 of group b / 8 (<= 128
+// rows per group), 16 lanes per (row, 128-k block) cell, four cells' loads
+// in flight per lane.
+template <bool BF>
+__global__ void __launch_bounds__(256) group_rowsum_tg_kernel(const uint16_t* __restrict__ x,
+                                                              int64_t stride, int K, float base,
+                                                              const int* __restrict__ hdr,
+                                                              const TgEntry* __restrict__ tg,
+                                                              int rs_rows, float* __restrict__ out) {
+  const int g = (int)(blockIdx.x >> 3), r0 = (int)(blockIdx.x & 7) * 16;
+  const int lo = hdr[3];
+  if (g >= hdr[0] - lo) return;
+  const TgEntry te = tg[lo + g];
+  const int nr = min(16, te.cnt - r0);
+  if (nr <= 0) return;
+  const int nblk = K / 128;                  // 128-k blocks per row
+  const int cells = nr * nblk;
+  const int lane16 = threadIdx.x & 15, c0 = threadIdx.x >> 4;
+  constexpr int U = 4;
+  for (int cb = 0; cb < cells; cb += 16 * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = cb + u * 16 + c0;
+      v[u] = make_uint4(0u, 0u, 0u, 0u);
+      if (c < cells) {
+        const int r = c / nblk, kb = c - r * nblk;
+        v[u] = *reinterpret_cast<const uint4*>(x + (int64_t)(te.pos0 + r0 + r) * stride +
+                                               kb * 128 + lane16 * 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t d[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if constexpr (BF)
+          sum += __uint_as_float(d[i] << 16) + __uint_as_float(d[i] & 0xffff0000u);
+        else
+          sum += f16_bits_to_f32(d[i] & 0xffffu) + f16_bits_to_f32(d[i] >> 16);
+      }
+      sum += __shfl_xor(sum, 1, 64);
+      sum += __shfl_xor(sum, 2, 64);
+      sum += __shfl_xor(sum, 4, 64);
+      sum += __shfl_xor(sum, 8, 64);
+      const int c = cb + u * 16 + c0;
+      if (c < cells && lane16 == 0) {
+        const int r = c / nblk, kb = c - r * nblk;
+        out[(int64_t)kb * rs_rows + te.pos0 + r0 + r] = base * sum;
+      }
+    }
+  }
+}
+
 // ---- kernels ------------------------------------------------------------------
 // Each stage array is its own LDS object, so the compiler can tell that reading
 // one stage cannot touch another's pending copy.
@@ -1093,6 +1150,22 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
     hipLaunchKernelGGL(group_rowsum_kernel<false>, dim3((unsigned)rows), dim3(256), 0, s, x,
                        stride, (int)rows, K, gs, -1032.0f, out);
   return check_launch("group_rowsum_kernel");
+}
+
+int launch_group_rowsum_tg(bool bf, const uint16_t* x, int64_t stride, int K, const int* hdr,
+                           const TgEntry* tg, int64_t cap, int64_t rs_rows, float* out,
+                           hipStream_t s) {
+  const int64_t grid = 8 * cap;
+  if (grid <= 0) return EXQ_SUCCESS;
+  if (grid > INT32_MAX || rs_rows > INT32_MAX)
+    return set_error(EXQ_ERROR_UNSUPPORTED, "group_rowsum_tg: too many rows");
+  if (bf)
+    hipLaunchKernelGGL(group_rowsum_tg_kernel<true>, dim3((unsigned)grid), dim3(256), 0, s, x,
+                       stride, K, -136.0f, hdr, tg, (int)rs_rows, out);
+  else
+    hipLaunchKernelGGL(group_rowsum_tg_kernel<false>, dim3((unsigned)grid), dim3(256), 0, s, x,
+                       stride, K, -1032.0f, hdr, tg, (int)rs_rows, out);
+  return check_launch("group_rowsum_tg_kernel");
 }
 
 template <int MODE>
