@@ -994,25 +994,29 @@ __global__ void __launch_bounds__(256) group_rowsum_kernel(const uint16_t* __res
 
 // The same sums for the expert-sorted rows of token groups [hdr[3], hdr[0])
 // only (the 64 x 256 INT4 tiles' groups; the scaled-operand and BF16 tiles
-// read none): work-group b takes rows 16 (b % 8) .. +15 of group b / 8 (<= 128
-// rows per group), 16 lanes per (row, 128-k block) cell, four cells' loads
-// in flight per lane.
+// read none): work-group b takes rows 8 (b % 16) .. +7 of group b / 16 (<= 128
+// rows per group), 16 lanes per (row, 128-k block) cell; a lane's loads for
+// up to eight cells go out together.
+constexpr int kRowsumTgRows = 8;
+constexpr int kRowsumTgParts = kTokenGroupI4 / kRowsumTgRows;
+
 template <bool BF>
 __global__ void __launch_bounds__(256) group_rowsum_tg_kernel(const uint16_t* __restrict__ x,
                                                               int64_t stride, int K, float base,
                                                               const int* __restrict__ hdr,
                                                               const TgEntry* __restrict__ tg,
                                                               int rs_rows, float* __restrict__ out) {
-  const int g = (int)(blockIdx.x >> 3), r0 = (int)(blockIdx.x & 7) * 16;
+  const int g = (int)(blockIdx.x / kRowsumTgParts);
+  const int r0 = (int)(blockIdx.x % kRowsumTgParts) * kRowsumTgRows;
   const int lo = hdr[3];
   if (g >= hdr[0] - lo) return;
   const TgEntry te = tg[lo + g];
-  const int nr = min(16, te.cnt - r0);
+  const int nr = min(kRowsumTgRows, te.cnt - r0);
   if (nr <= 0) return;
-  const int nblk = K / 128;                  // 128-k blocks per row
+  const int nblk = K / 128;  // 128-k blocks per row
   const int cells = nr * nblk;
   const int lane16 = threadIdx.x & 15, c0 = threadIdx.x >> 4;
-  constexpr int U = 4;
+  constexpr int U = 8;
   for (int cb = 0; cb < cells; cb += 16 * U) {
     uint4 v[U];
 #pragma unroll
@@ -1155,7 +1159,7 @@ int launch_group_rowsum(bool bf, const uint16_t* x, int64_t stride, int64_t rows
 int launch_group_rowsum_tg(bool bf, const uint16_t* x, int64_t stride, int K, const int* hdr,
                            const TgEntry* tg, int64_t cap, int64_t rs_rows, float* out,
                            hipStream_t s) {
-  const int64_t grid = 8 * cap;
+  const int64_t grid = kRowsumTgParts * cap;
   if (grid <= 0) return EXQ_SUCCESS;
   if (grid > INT32_MAX || rs_rows > INT32_MAX)
     return set_error(EXQ_ERROR_UNSUPPORTED, "group_rowsum_tg: too many rows");

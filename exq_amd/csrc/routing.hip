@@ -225,36 +225,37 @@ struct WideLds {
   uint32_t masks[MASK_WORDS];
 };
 
-// hist[key(i)] += 1 for i in [a, z): keys are loaded eight per thread before
-// their LDS atomics, so the loads are in flight together.
-template <typename KeyFn>
-__device__ __forceinline__ void count_range(int a, int z, KeyFn key, int* hist) {
-  constexpr int U = 8;
-  for (int64_t i0 = a; i0 < z; i0 += RT * U) {
-    int kv[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + u * RT + (int)threadIdx.x;
-      kv[u] = i < z ? key((int)i) : -1;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (kv[u] >= 0) atomicAdd(&hist[kv[u]], 1);
-  }
-}
-
 // tot[] (all n items) and before[] (the items before lo) per bucket; each
 // item costs one LDS atomic (the items from lo on count into tot, which then
-// adds before).
+// adds before).  Sixteen keys per thread are loaded before their atomics, so
+// up to 16,384 items take one memory round trip.  *own receives the key of
+// item lo + threadIdx.x when lo is a multiple of RT (-1 past n), for a
+// scatter of [lo, lo + RT) that then needs no second load.
 template <typename KeyFn>
-__device__ void wide_count(int n, int lo, int nb, KeyFn key, int* tot, int* before) {
+__device__ void wide_count(int n, int lo, int nb, KeyFn key, int* tot, int* before,
+                           int* own = nullptr) {
   for (int b = threadIdx.x; b < nb; b += RT) {
     tot[b] = 0;
     before[b] = 0;
   }
   __syncthreads();
-  count_range(0, lo < n ? lo : n, key, before);
-  count_range(lo, n, key, tot);
+  constexpr int U = 16;
+  int mine = -1;
+  for (int64_t i0 = 0; i0 < n; i0 += (int64_t)RT * U) {
+    int kv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + u * RT + (int)threadIdx.x;
+      kv[u] = i < n ? key((int)i) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i0u = i0 + u * RT;
+      if (i0u == lo) mine = kv[u];
+      if (kv[u] >= 0) atomicAdd(i0u + (int)threadIdx.x < lo ? &before[kv[u]] : &tot[kv[u]], 1);
+    }
+  }
+  if (own) *own = mine;
   __syncthreads();
   for (int b = threadIdx.x; b < nb; b += RT) tot[b] += before[b];
   __syncthreads();
@@ -541,7 +542,8 @@ __global__ void __launch_bounds__(RT) route_plan_recount_kernel(RoutePlanParams 
   const int nb = p.Ep;
   const bool tail = blockIdx.x == gridDim.x - 1;
   const int lo = tail ? p.n : blockIdx.x * per, hi = min(p.n, lo + per);
-  wide_count(p.n, lo, nb, key, s.cnt, s.run);
+  int own;  // key of slot lo + threadIdx.x (per == RT: lo is a multiple of RT)
+  wide_count(p.n, lo, nb, key, s.cnt, s.run, &own);
   const int b = threadIdx.x;
   int t;
   const int ex = block_excl_scan(b < nb ? s.cnt[b] : 0, s.wsum, &t);
@@ -555,7 +557,11 @@ __global__ void __launch_bounds__(RT) route_plan_recount_kernel(RoutePlanParams 
     plan_tail(p, s);
     return;
   }
-  wide_scatter(lo, hi, nb, key, s.run, s.masks, [&](int i, int bk, int pos) {
+  const bool cached = per == RT;
+  auto key_or_own = [&](int slot) {
+    return cached && slot == lo + (int)threadIdx.x ? own : plan_key(p, slot);
+  };
+  wide_scatter(lo, hi, nb, key_or_own, s.run, s.masks, [&](int i, int bk, int pos) {
     p.sorted[pos] = i;
     if (p.sort_order_out && bk < p.E) p.sort_order_out[pos] = routed_slot(p, i);
   });
