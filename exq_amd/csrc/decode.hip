@@ -780,41 +780,49 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Rows& row
   }
 }
 
-// LDS-path unit with the slice copied k-block by k-block into separate LDS
-// arrays (one per k-block position, all four waves' copies), so that the
-// k-loop starts on k-block 0 while later k-blocks are still landing: the
-// copies go out in the order scales, k-block 0, activations 0-1, k-blocks
-// 1.., and each k-block waits only for the loads issued up to it.  A wave
-// always issues CK k-block copies (through an empty buffer past its range),
-// so those waits are fixed counts.  Separate arrays let the compiler see
-// that reading one k-block cannot touch another's pending copy.  The partial
-// tiles go to k-block 0's array once the loop is done.
+// LDS-path unit with the slice copied a pair of k-blocks at a time into
+// separate LDS arrays (one per pair position, all four waves' copies), so
+// that the k-loop starts on the first pair while the second is still
+// landing: the copies go out in the order scales, pair 0, activations 0-1,
+// pair 1, and each k-block waits only for the loads issued up to it.  One
+// copy instruction moves 8 rows x 128 bytes (two k-blocks of each row: whole
+// cache lines, as a streaming read fetches them), into LDS rows of eight
+// 16-byte pieces, piece c of row r at c ^ ((r >> 1) & 7) (conflict-free MFMA
+// operand reads).  A wave always issues CK / 2 pair copies (through an empty
+// buffer past its range, zeros for a range's odd last k-block), so those
+// waits are fixed counts.  Separate arrays let the compiler see that reading
+// one pair cannot touch another's pending copy.  A slice that only this unit
+// reads (its expert has one 16-row tile) is copied with the nontemporal hint.
+// The partial tiles go to pair 0's array once the loop is done.
 template <bool BF, int PH, typename Rows>
 __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Rows& rows, int e, int blk,
-                                            int sp, int tile, bool prio) {
+                                            int sp, int tile, bool prio, bool once) {
   constexpr int NT = 1;
   using G = Geo<2, PH, NT>;
   constexpr int RS = G::RS, CK = G::CK;
-  static_assert(CK == 2 || CK == 4, "k-block arrays");
-  constexpr int KBB = RS * 1024;  // one k-block of the wave's rows
-  __shared__ __attribute__((aligned(16))) unsigned char s_kb0[DW * KBB];
-  __shared__ __attribute__((aligned(16))) unsigned char s_kb1[DW * KBB];
-  __shared__ __attribute__((aligned(16))) unsigned char s_kb2[CK > 2 ? DW * KBB : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char s_kb3[CK > 2 ? DW * KBB : 16];
+  static_assert(CK == 2 || CK == 4, "k-block pairs");
+  constexpr int KPB = 2 * RS * 1024;  // one pair of k-blocks of the wave's rows
+  constexpr int NP = CK / 2;          // pair arrays
+  __shared__ __attribute__((aligned(16))) unsigned char s_kp0[DW * KPB];
+  __shared__ __attribute__((aligned(16))) unsigned char s_kp1[NP > 1 ? DW * KPB : 16];
   __shared__ __attribute__((aligned(16))) unsigned char s_sc[DW * WAVE_S];
   const UnitCtx<2, PH, NT> u(a, e, blk, sp);
-  auto kbuf = [&](int kbl) {
-    return (kbl == 0 ? s_kb0 : kbl == 1 ? s_kb1 : kbl == 2 ? s_kb2 : s_kb3) + u.wave * KBB;
-  };
-  // k-block kbl of the wave's range: RS instructions of 16 rows x 4 pieces;
-  // LDS piece (row, c') holds source piece c' ^ (row & 3)
-  const int dr = u.lane >> 2, dc = (u.lane & 3) ^ (dr & 3);
-  auto copy_kb = [&](int kbl) {
-    const bool ok = uni_b(kbl < u.nmy);
+  auto pbuf = [&](int pp) { return (pp == 0 ? s_kp0 : s_kp1) + u.wave * KPB; };
+  // pair pp of the wave's range: 2 * RS instructions of 8 rows x 8 pieces
+  const int prow = u.lane >> 3;
+  auto copy_pair = [&](int pp) {
+    const bool any = uni_b(2 * pp < u.nmy);
 #pragma unroll
-    for (int rs = 0; rs < RS; ++rs)
-      dma16(ok ? u.wr : u.wnull, kbuf(kbl) + rs * 1024,
-            ok ? u.row(a, blk, rs * 16 + dr) * u.rowbytes + (u.lo + kbl) * 64 + dc * 16 : 0);
+    for (int j = 0; j < 2 * RS; ++j) {
+      const int r = j * 8 + prow;
+      const int c = (u.lane & 7) ^ ((r >> 1) & 7);  // source piece of this LDS slot
+      const bool in = 2 * pp + (c >> 2) < u.nmy;
+      const int off = in ? u.row(a, blk, r) * u.rowbytes + (u.lo + 2 * pp) * 64 + c * 16 : OOB_OFF;
+      if (once)
+        dma16_nt(any ? u.wr : u.wnull, pbuf(pp) + j * 1024, any ? off : 0);
+      else
+        dma16(any ? u.wr : u.wnull, pbuf(pp) + j * 1024, any ? off : 0);
+    }
   };
   unsigned char* scl = s_sc + u.wave * WAVE_S;
   // With three or more units per work-group, the copies go out at raised
@@ -834,7 +842,7 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Rows& rows
     const bool in = u.lane * 16 < RS * blk_bytes;
     dma16(u.sr, scl, in ? goff : OOB_OFF);
   }
-  copy_kb(0);
+  copy_pair(0);
   const int r_begin = tile * 16;
   int sl[NT];
   const int cnt = __builtin_amdgcn_readfirstlane(rows.template slots<NT>(a, e, r_begin, sl));
@@ -851,8 +859,7 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Rows& rows
   };
   load_a(0, 0);
   load_a(1, 1);
-#pragma unroll
-  for (int kbl = 1; kbl < CK; ++kbl) copy_kb(kbl);
+  if constexpr (NP > 1) copy_pair(1);
   if (prio) __builtin_amdgcn_s_setprio(0);
 
   const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
@@ -863,30 +870,31 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Rows& rows
   f32x4_t tot[RS];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs) tot[rs] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // Loads in flight behind k-block kbl's copy, in issue order: for kbl = 0
-  // the second activation fragments and copies 1..CK-1; for kbl >= 1 the
-  // later copies and the activation loads issued in the loop (k-blocks 2..,
-  // issued after every copy, so they never count as behind a copy).
+  const int pswz = (u.r16 >> 1) & 7;  // rows rs * 16 + r16 share it
+  // Loads in flight behind k-block kbl's operands, in issue order: for kbl = 0
+  // the second activation fragments and pair 1; for kbl = 1 pair 1 and k-block
+  // 2's activations (issued in the loop after pair 1); for kbl = 2 k-block 3's
+  // activations.
 #pragma unroll
   for (int kbl = 0; kbl < CK; ++kbl) {
     const int p = kbl & 1;
     if (kbl == 0) {
-      wait_vm_le<4 + (CK - 1) * RS>();
-    } else if (kbl == 1) {
-      wait_vm_le<(CK - 2) * RS + (CK > 2 ? 4 : 0)>();  // + k-block 2's activations
+      wait_vm_le<4 + (NP > 1 ? 2 * RS : 0)>();
+    } else if (kbl == 1 && NP > 1) {
+      wait_vm_le<2 * RS + 4>();
     } else if (kbl == 2) {
-      wait_vm_le<4>();  // k-block 3's activations
+      wait_vm_le<4>();
     } else {
       wait_vm_all();
     }
     uint4 xa[4];
     f32x4_t init;
     make_a<2, BF, PH>(areg[p], xa, init);
-    const unsigned char* kb_lds = kbuf(kbl);
+    const unsigned char* kp_lds = pbuf(kbl >> 1);
+    const int poff = ((((kbl & 1) * 4 + u.kq) ^ pswz)) * 16;
 #pragma unroll
     for (int rs = 0; rs < RS; ++rs) {
-      const uint4 w = *reinterpret_cast<const uint4*>(
-          kb_lds + rs * 1024 + (u.r16 * 4 + (u.kq ^ (u.r16 & 3))) * 16);
+      const uint4 w = *reinterpret_cast<const uint4*>(kp_lds + (rs * 16 + u.r16) * 128 + poff);
       f32x4_t acc = dmfma<BF>(xa[0], ddeq4(w.x, dq_mask, dq_magic), init);
       acc = dmfma<BF>(xa[1], ddeq4(w.y, dq_mask, dq_magic), acc);
       acc = dmfma<BF>(xa[2], ddeq4(w.z, dq_mask, dq_magic), acc);
@@ -899,14 +907,14 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Rows& rows
     }
     if (kbl + 2 < CK) load_a(p, kbl + 2);
   }
-  // partial tiles into k-block 0's array (this wave's reads of it are done)
+  // partial tiles into pair 0's array (this wave's reads of it are done)
   wave_lds_fence();
-  float4* red = reinterpret_cast<float4*>(kbuf(0));
+  float4* red = reinterpret_cast<float4*>(pbuf(0));
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs)
     red[rs * 64 + u.lane] = float4{tot[rs][0], tot[rs][1], tot[rs][2], tot[rs][3]};
   __syncthreads();
-  finish_pass<2, BF, PH, NT, KBB>(a, u, s_kb0, sl, cc, 1, blk);
+  finish_pass<2, BF, PH, NT, KPB>(a, u, s_kp0, sl, cc, 1, blk);
   __syncthreads();  // LDS arrays free again
 }
 
@@ -1248,12 +1256,12 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Rows& ro
 template <bool BF, int PH, int NT, bool MIXED, int PATH, typename Rows>
 __device__ __forceinline__ void run_unit_any(const LayerArgs& a, const Rows& rows, const Route* rt,
                                              int e, int blk, int sp, int t, uint32_t ev,
-                                             unsigned char* dyn_lds, bool prio) {
+                                             unsigned char* dyn_lds, bool prio, bool once) {
   const int tier = (int)(ev >> 30);
   const int widx = MIXED ? (int)(ev & kRowMask) : -1;
   if (!MIXED || tier == 2) {
     if constexpr (PATH == 1 && NT == 1 && !MIXED)
-      run_unit_kb<BF, PH>(a, rows, e, blk, sp, t, prio);
+      run_unit_kb<BF, PH>(a, rows, e, blk, sp, t, prio, once);
     else if constexpr (PATH == 1)
       run_unit_dma<BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx);
     else if constexpr (PATH == 2 && PH == 0)
@@ -1368,8 +1376,10 @@ __device__ __forceinline__ void decode_gateup(const LayerArgs& a, unsigned char*
     int e, blk, t;
     decode(u, e, blk, t);
     const uint32_t ev = MIXED ? (uint32_t)__builtin_amdgcn_readfirstlane(emap[e]) : (2u << 30);
+    // the expert's only 16-row tile reads its slice once
+    const bool once = expert_rows(cntw, e) <= 16;
     run_unit_any<BF, PH, NT, MIXED, PATH>(a, rows, &rt, e, blk, 0, t, ev, dyn_lds,
-                                         n_units > 2 * (int)gridDim.x);
+                                         n_units > 2 * (int)gridDim.x, once);
   }
   // The down kernel's plan, after this work-group's own units (the last
   // work-groups of the grid hold the fewest units); the routing state in LDS
@@ -1410,7 +1420,7 @@ __device__ __forceinline__ void decode_down(const LayerArgs& a, unsigned char* d
     const RowsPlan rows{__builtin_amdgcn_readfirstlane(h.y), slot};
     const uint32_t ev = MIXED ? (uint32_t)__builtin_amdgcn_readfirstlane(h.z) : (2u << 30);
     run_unit_any<BF, PH, NT, MIXED, PATH>(a, rows, nullptr, e, blk, sp, t, ev, dyn_lds,
-                                         n_units > 2 * (int)gridDim.x);
+                                         n_units > 2 * (int)gridDim.x, rows.cnt <= 16);
     if (a.combine) publish_and_combine<BF, rows_b(NT)>(a, blk, n_tiles, &s_flag);
     u += gridDim.x;
     if (u < n_units) {

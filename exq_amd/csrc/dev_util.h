@@ -117,6 +117,14 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, unsigned char* l
 #endif
 }
 
+// The same with the nontemporal hint (`nt`): for bytes read once, whose lines
+// need not stay in the caches.
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)lds, 16, voff, 0, 0, 2);
+#endif
+}
+
 // 4 bytes per lane into LDS at lds + 4 * lane (buffer_load_dword ... lds).
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, unsigned char* lds, int voff) {
 #if defined(__HIP_DEVICE_COMPILE__)
