@@ -663,7 +663,7 @@ def stream_read_ceiling(dev, nbytes=2 << 30, reps=10):
     cross = stream_cross_check(buf, reps)
     del buf, sink
     return {"GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes, "reps": reps,
-            "kernel": "exq_stream_read (16-byte loads, 8 in flight per thread)",
+            "kernel": "exq_stream_read (16-byte nontemporal loads, 8 in flight per thread)",
             "cross_check": cross}
 
 

@@ -662,7 +662,8 @@ __device__ __forceinline__ void publish_and_combine(const LayerArgs& a, int blk,
 // register ring.
 template <bool BF, int PH, int NT, typename Rows>
 __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Rows& rows, int e, int blk,
-                                             int sp, int tile, unsigned char* lds, int widx = -1) {
+                                             int sp, int tile, unsigned char* lds, int widx,
+                                             bool once) {
   using G = Geo<2, PH, NT>;
   constexpr int RS = G::RS, CK = G::CK;
   constexpr int DA = NT == 4 ? 1 : 2;  // activation k-blocks in flight
@@ -675,7 +676,11 @@ __device__ __forceinline__ void run_unit_dma(const LayerArgs& a, const Rows& row
       const int p = j * 64 + u.lane;
       const int rr = p / p4;
       const int c = (p - rr * p4) ^ (rr & xm);
-      dma16(u.wr, region + j * 1024, u.row(a, blk, rr) * u.rowbytes + u.lo * 64 + c * 16);
+      const int off = u.row(a, blk, rr) * u.rowbytes + u.lo * 64 + c * 16;
+      if (once)  // a slice this unit alone reads: nontemporal
+        dma16_nt(u.wr, region + j * 1024, off);
+      else
+        dma16(u.wr, region + j * 1024, off);
     }
   };
   auto wslot = [&](int kbl, int rs) {  // LDS byte offset of this lane's piece
@@ -928,7 +933,8 @@ __device__ __forceinline__ void run_unit_kb(const LayerArgs& a, const Rows& rows
 // (row r's groups g_lo.. as nd dwords from its aligned start).
 template <bool BF, int NT>
 __device__ __forceinline__ void run_unit_dma_chunked(const LayerArgs& a, const Route& rt, int e,
-                                                     int blk, int tile, unsigned char* lds) {
+                                                     int blk, int tile, unsigned char* lds,
+                                                     bool once) {
   constexpr int PH = 0;
   using G = Geo<2, PH, NT>;
   constexpr int RS = G::RS, CK = G::CK;
@@ -985,7 +991,11 @@ __device__ __forceinline__ void run_unit_dma_chunked(const LayerArgs& a, const R
         const int p = j * 64 + u.lane;
         const int rr = p / p4;
         const int c = (p - rr * p4) ^ (rr & xm);
-        dma16(u.wr, region + j * 1024, u.row(a, blk, rr) * u.rowbytes + (u.lo + c0) * 64 + c * 16);
+        const int off = u.row(a, blk, rr) * u.rowbytes + (u.lo + c0) * 64 + c * 16;
+        if (once)  // a slice this unit alone reads: nontemporal
+          dma16_nt(u.wr, region + j * 1024, off);
+        else
+          dma16(u.wr, region + j * 1024, off);
       }
       uint4 areg[DA][4 * NT];
       auto load_a = [&](int p, int kbl) {  // zeros past the chunk
@@ -1263,9 +1273,9 @@ __device__ __forceinline__ void run_unit_any(const LayerArgs& a, const Rows& row
     if constexpr (PATH == 1 && NT == 1 && !MIXED)
       run_unit_kb<BF, PH>(a, rows, e, blk, sp, t, prio, once);
     else if constexpr (PATH == 1)
-      run_unit_dma<BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx);
+      run_unit_dma<BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx, once);
     else if constexpr (PATH == 2 && PH == 0)
-      run_unit_dma_chunked<BF, NT>(a, *rt, e, blk, t, dyn_lds);
+      run_unit_dma_chunked<BF, NT>(a, *rt, e, blk, t, dyn_lds, once);
     else
       run_unit_ring<2, BF, PH, NT>(a, rows, e, blk, sp, t, dyn_lds, widx);
   } else if constexpr (MIXED) {
