@@ -1659,8 +1659,9 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
     for (int d = 0; d < 4; ++d)
       xv[i][d] = __builtin_bit_cast(
           uint4, __builtin_amdgcn_raw_buffer_load_b128(xr, ok ? (c * 32 + d * 8) * 2 : OOB_OFF, 0, 0));
-    gw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(gr, ok ? c * 16 : OOB_OFF, 0, 0));
-    uw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ur, ok ? c * 16 : OOB_OFF, 0, 0));
+    // one token: every weight row is read once, nontemporal (aux 2)
+    gw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(gr, ok ? c * 16 : OOB_OFF, 0, 2));
+    uw[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ur, ok ? c * 16 : OOB_OFF, 0, 2));
     gs[i] = __builtin_amdgcn_raw_buffer_load_b16(gsr, ok ? (c / gch) * 2 : OOB_OFF, 0, 0);
     us[i] = __builtin_amdgcn_raw_buffer_load_b16(usr, ok ? (c / gch) * 2 : OOB_OFF, 0, 0);
   }
@@ -1721,7 +1722,7 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
 // as stored, against `mid` put back in natural order; INT8 bytes become exact
 // 16-bit pairs and the row's fp16 scale multiplies the sum).  NCH: 32-k chunks
 // per lane (all of a lane's loads are issued before its arithmetic).
-template <bool BF, bool MIXED, int NCH>
+template <bool BF, bool MIXED, int NCH, bool ONCE>  // ONCE: one token, each weight row read once
 __global__ void __launch_bounds__(256) decode_down_rows_kernel(LayerArgs a) {
   constexpr int R = ROWS_R;
   __shared__ float red[ROWS_MAX_SLOTS][R];
@@ -1780,8 +1781,10 @@ __global__ void __launch_bounds__(256) decode_down_rows_kernel(LayerArgs a) {
           const int c = l + 32 * i;
 #pragma unroll
           for (int r = 0; r < R; ++r) {
-            w[i][r] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    wr, c < C ? r * rowb + c * 16 : OOB_OFF, 0, 0));
+            // at one token each weight row is read once: nontemporal (aux 2)
+            w[i][r] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, c < C ? r * rowb + c * 16 : OOB_OFF,
+                                                             0, ONCE ? 2 : 0));
             sc[i][r] = __builtin_amdgcn_raw_buffer_load_b16(sr, c < C ? (r * ng + c / gch) * 2 : OOB_OFF, 0, 0);
           }
         }
@@ -1989,6 +1992,15 @@ bool decode_path_supported(int64_t T, int64_t k, int64_t Ep, int64_t n_shared, i
   return ring_scales_fit(H, 32) && ring_scales_fit(I, rows_b(1));
 }
 
+// decode_down_rows_kernel for nch 32-k chunks per lane (1 or 2), nontemporal
+// weight loads when every weight row is read once (one token).
+template <bool BF, bool MIXED>
+static decode_kernel_t pick_down_rows(int nch, bool once) {
+  if (nch <= 1)
+    return once ? decode_down_rows_kernel<BF, MIXED, 1, true> : decode_down_rows_kernel<BF, MIXED, 1, false>;
+  return once ? decode_down_rows_kernel<BF, MIXED, 2, true> : decode_down_rows_kernel<BF, MIXED, 2, false>;
+}
+
 int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
   LayerArgs a{};
   a.ids = d.ids;
@@ -2044,13 +2056,10 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
       // few tokens: the down projection by output rows, summed in-kernel
       const dim3 g1((unsigned)(d.H / ROWS_R));
       const int nch = (d.I / 32 + 31) / 32;  // chunks per lane
-      decode_kernel_t k1;
-      if (mixed)
-        k1 = nch <= 1 ? (d.bf ? decode_down_rows_kernel<true, true, 1> : decode_down_rows_kernel<false, true, 1>)
-                      : (d.bf ? decode_down_rows_kernel<true, true, 2> : decode_down_rows_kernel<false, true, 2>);
-      else
-        k1 = nch <= 1 ? (d.bf ? decode_down_rows_kernel<true, false, 1> : decode_down_rows_kernel<false, false, 1>)
-                      : (d.bf ? decode_down_rows_kernel<true, false, 2> : decode_down_rows_kernel<false, false, 2>);
+      const decode_kernel_t k1 =
+          mixed ? (d.bf ? pick_down_rows<true, true>(nch, d.T == 1) : pick_down_rows<false, true>(nch, d.T == 1))
+                : (d.bf ? pick_down_rows<true, false>(nch, d.T == 1)
+                        : pick_down_rows<false, false>(nch, d.T == 1));
       if (ev)
         hipExtLaunchKernelGGL(k1, g1, dim3(256), 0, s, ev[2], ev[3], 0, a);
       else
