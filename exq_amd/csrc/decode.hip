@@ -1073,10 +1073,16 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Rows& ro
   constexpr int NPASS = RS / RSP;
   using pass0_t = std::integral_constant<int, 0>;
   const UnitCtx<TIER, PH, NT> u(a, e, blk, sp, widx);
+  // A lane's 16-byte weight loads of a k-block: INT4 (one) at kq * 16; BF16 /
+  // INT8 (four / two) at kq * 16 + h * 64, so that each load instruction reads
+  // 64 contiguous bytes of every row and the lane holds, for MFMA step d, k
+  // = 32 d + 8 kq .. (BF16) or 64 (d / 2) + 16 kq + 8 (d % 2) .. (INT8); the
+  // activation fragments are read in the same k order (a_off below).
+  constexpr int WSTEP = TIER == 2 ? 16 : 64;
   int voff[RS];
 #pragma unroll
   for (int rs = 0; rs < RS; ++rs)
-    voff[rs] = u.row(a, blk, rs * 16 + u.r16) * u.rowbytes + u.kq * 16 * QPK;
+    voff[rs] = u.row(a, blk, rs * 16 + u.r16) * u.rowbytes + u.kq * 16;
   const uint32_t dq_mask = __builtin_amdgcn_readfirstlane(0x000F000Fu);
   uint32_t dq_magic = BF ? 0x43004300u : 0x64006400u;
   asm volatile("" : "+v"(dq_magic));
@@ -1122,8 +1128,15 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Rows& ro
 #pragma unroll
       for (int h = 0; h < QPK; ++h)
         wreg[p][rs * QPK + h] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff[rs0 + rs] + h * 16, kb * G::KBSTRIDE, 0));
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff[rs0 + rs] + h * WSTEP, kb * G::KBSTRIDE, 0));
     }
+  };
+  // byte offset of step d's activation fragment from the lane's row start
+  // (u.xoff puts lane kq at k = 32 kq, the INT4 order)
+  auto a_off = [&](int d) {
+    if constexpr (TIER == 2) return d * 16;
+    else if constexpr (TIER == 0) return d * 64 - u.kq * 48;
+    else return (d >> 1) * 128 + (d & 1) * 16 - u.kq * 32;
   };
   auto load_a = [&](int p, int kbl) {
     const bool ok = uni_b(kbl < u.nmy);
@@ -1133,7 +1146,7 @@ __device__ __forceinline__ void run_unit_ring(const LayerArgs& a, const Rows& ro
 #pragma unroll
       for (int d = 0; d < 4; ++d)
         areg[p][tt * 4 + d] = __builtin_bit_cast(
-            uint4, __builtin_amdgcn_raw_buffer_load_b128(ok ? u.xr : u.xnull, xo[tt] + d * 16,
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(ok ? u.xr : u.xnull, xo[tt] + a_off(d),
                                                          kb * 256, 0));
   };
 
