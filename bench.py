@@ -22,7 +22,7 @@ launch (48 distinct buffers replayed from a graph: the floor at that
 transfer size) and the reference's CPU path timed on this host at every
 configuration, both variants (`cpu_baseline.configs`).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 25] [--batch 16]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 100] [--batch 16]
                     [--sweep 1,4,16,64] [--layers 48] [--no-cpu] [--no-configs]
 
 Counter runs (HBM traffic of the dominant kernel, rocprofv3 --pmc), one per
@@ -57,9 +57,10 @@ def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    # 25 steps of 48 Qwen3 layers at T=16 are about 40 ms: the clocks have
-    # settled before the timed steps (WARMUP_MS)
-    ap.add_argument("--warmup", type=int, default=25)
+    # 100 steps of 48 Qwen3 layers at T=16 are about 150 ms: the clocks have
+    # settled before the timed steps, also after the long idle spell of
+    # building the stack (25 steps left the P95 step 10 % above the P50)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--sweep", type=str, default="1,4,16,64")
     ap.add_argument("--layers", type=int, default=48)

@@ -400,11 +400,15 @@ struct UnitCtx {
     K = PH == 0 ? a.H : a.I;
     nkb = K >> 7;
     split = sp;
-    // the split's k-blocks [s0, s1), then this wave's quarter of them
+    // the split's k-blocks [s0, s1), then this wave's quarter of them; the
+    // longer ranges go to the first waves, so that with two k-blocks copied
+    // per instruction the ranges start at even k-blocks where they can (six
+    // k-blocks: 2, 2, 1, 1 from k-blocks 0, 2, 4, 5)
     const int ns = PH == 0 ? 1 : a.nsplit;
     const int s0 = (sp * nkb) / ns, s1 = ((sp + 1) * nkb) / ns;
-    lo = s0 + ((wave * (s1 - s0)) >> 2);
-    nmy = s0 + (((wave + 1) * (s1 - s0)) >> 2) - lo;  // k-blocks of this wave
+    const int nq = (s1 - s0) >> 2, nx = (s1 - s0) & 3;
+    lo = s0 + wave * nq + (wave < nx ? wave : nx);
+    nmy = nq + (wave < nx ? 1 : 0);  // k-blocks of this wave
     const Proj& W = PH == 0 ? a.w13 : a.w2;
     const int n_rows = PH == 0 ? 2 * a.I : a.H;
     // the expert's row in its tier's bank (from the LDS map when the caller has it)
