@@ -369,7 +369,8 @@ int exq_set_stage_events(void* const* events, int n_events);
 
 /*
  * Measurement hook (no counterpart in the reference): the streaming-read
- * ceiling.  Reads `bytes` (a multiple of 16) from `buf` with 16-byte loads,
+ * ceiling.  Reads `bytes` (a multiple of 16) from `buf` with 16-byte
+ * nontemporal loads (faster from HBM than the default cache policy),
  * grid-strided over min(sink_words, 8192) work-groups of 256 threads, and
  * XORs each work-group's fold into sink[work-group] (so nothing is dead);
  * bench.py times it on a buffer far larger than the Infinity Cache to report
