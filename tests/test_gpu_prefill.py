@@ -153,6 +153,25 @@ def test_prefill_per_expert_tile_shape_mixed_bank(act, device):
                      f"prefill per-expert tile shape mixed bank {act}")
 
 
+def test_prefill_per_expert_tile_shape_none_big(device):
+    """A batch of 512 tokens (the per-expert switch is on) whose experts all stay
+    below 384 rows: the 128 x 256 range of the combined launch is empty and every
+    INT4 group takes the 64 x 256 tiles."""
+    from exq_amd.kernels import fused_experts
+    cfg = synth.MoeConfig("prefill_none_big", 52, 1024, 512, 32, 2, True, zipf=False)
+    T = 512
+    banner("prefill per-expert tile shape, no big expert")
+    p13, s13, p2, s2 = _pack(cfg.n_experts, cfg.inter, cfg.hidden, 986, device)
+    ids, w = synth.routing(cfg, T)
+    counts = np.bincount(ids.reshape(-1), minlength=cfg.n_experts)
+    assert counts.max() < 384 and T * cfg.top_k < 512 * cfg.n_experts
+    x = _hidden(T, cfg.hidden, 987, device, torch.bfloat16)
+    out = fused_experts(x, p13, s13, p2, s2, torch.from_numpy(w).to(device),
+                        torch.from_numpy(ids).to(device))
+    ref = oracle_int4_layer(x, p13, s13, p2, s2, ids, w)
+    assert_close_rel(out, ref, TOL, "prefill per-expert tile shape, no big expert")
+
+
 def test_prefill_group_size_256_untiled(device):
     """group_size 256 is not tiled: the 64-row grouped kernel runs instead."""
     from exq_amd.kernels import fused_experts
