@@ -1629,16 +1629,17 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 
 // The gate/up projection for the same batches, by output rows: work-group
 // (x, y) takes routed slot y and the GU_PAIRS (gate j, up I + j) row pairs
-// j = x * GU_PAIRS + hw, one per half-wave.  A slot's expert is one load of
-// its id (no active-expert list is needed).  Lanes take the 32-k chunks
-// c = lane, lane + 32, ... of the token's row of x, permuted into the nibbles'
-// pairing order, and dot2 both rows' dequantised nibbles against it (as in
+// j = x * GU_PAIRS + w, one per wave.  A slot's expert is one load of its id
+// (no active-expert list is needed).  Lanes take the 32-k chunks c = lane,
+// lane + 64, ... of the token's row of x, permuted into the nibbles' pairing
+// order, and dot2 both rows' dequantised nibbles against it (as in
 // decode_down_rows_kernel); the folded gate and up sums give SiLU(g) * u, stored
 // in `mid` in INT4 pairing order.
-constexpr int GU_PAIRS = 8;
+constexpr int GU_PAIRS = 4;            // = waves per work-group
+constexpr int GU_THREADS = GU_PAIRS * 64;
 
-template <bool BF, int NCH>  // NCH >= ceil(H / 1024): 32-k chunks per lane, all loads issued first
-__global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
+template <bool BF, int NCH>  // NCH >= ceil(H / 2048): 32-k chunks per lane, all loads issued first
+__global__ void __launch_bounds__(GU_THREADS) decode_gateup_rows_kernel(LayerArgs a) {
   const int s = blockIdx.y;  // routed slot t * kp + j
   const int t = s / a.kp, js = s - t * a.kp;
   int e;
@@ -1649,8 +1650,8 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
   } else {
     e = a.E + (js - a.k);  // shared expert
   }
-  const int lane = threadIdx.x & 63, hw = threadIdx.x >> 5, l = threadIdx.x & 31;
-  const int j = blockIdx.x * GU_PAIRS + hw;  // gate row j, up row I + j
+  const int lane = threadIdx.x & 63, l = lane;
+  const int j = blockIdx.x * GU_PAIRS + (threadIdx.x >> 6);  // gate row j, up row I + j
   const int C = a.H >> 5;
   const int gch = 4 << a.gshift;
   const int ng = a.H >> (7 + a.gshift);
@@ -1669,8 +1670,8 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
   uint4 xv[NCH][4], gw[NCH], uw[NCH];
   uint32_t gs[NCH], us[NCH];
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {  // chunk c = l + 32 i; past C the loads return zero
-    const int c = l + 32 * i;
+  for (int i = 0; i < NCH; ++i) {  // chunk c = l + 64 i; past C the loads return zero
+    const int c = l + 64 * i;
     const bool ok = c < C;
 #pragma unroll
     for (int d = 0; d < 4; ++d)
@@ -1727,11 +1728,9 @@ __global__ void __launch_bounds__(256) decode_gateup_rows_kernel(LayerArgs a) {
   float g_lo, g_hi, u_lo, u_hi;
   fold(g, g_lo, g_hi);
   fold(u, u_lo, u_hi);
-  if (lane == 0) {  // this wave's two row pairs j0 = j (lo) and j0 + 1 (hi)
-    const int j0 = blockIdx.x * GU_PAIRS + 2 * (threadIdx.x >> 6);
+  if (lane == 0) {  // this wave's row pair: both half-waves' sums
     uint16_t* mrow = a.mid + (int64_t)s * a.I;
-    mrow[(j0 & ~7) + pair_pos(j0 & 7)] = (uint16_t)to_act_bits<BF>(silu_f32(g_lo) * u_lo);
-    mrow[((j0 + 1) & ~7) + pair_pos((j0 + 1) & 7)] = (uint16_t)to_act_bits<BF>(silu_f32(g_hi) * u_hi);
+    mrow[(j & ~7) + pair_pos(j & 7)] = (uint16_t)to_act_bits<BF>(silu_f32(g_lo + g_hi) * (u_lo + u_hi));
   }
 }
 
@@ -2057,14 +2056,14 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     if (ph == 0 && rows_gu) {
       // few tokens: the gate/up projection by output rows
       const dim3 g0((unsigned)(d.I / GU_PAIRS), (unsigned)(d.T * d.kp));
-      const int nch = (d.H / 32 + 31) / 32;  // chunks per lane
+      const int nch = (d.H / 32 + 63) / 64;  // chunks per lane
       const auto k0 = nch <= 1 ? (d.bf ? decode_gateup_rows_kernel<true, 1> : decode_gateup_rows_kernel<false, 1>)
                     : nch <= 2 ? (d.bf ? decode_gateup_rows_kernel<true, 2> : decode_gateup_rows_kernel<false, 2>)
                                : (d.bf ? decode_gateup_rows_kernel<true, 4> : decode_gateup_rows_kernel<false, 4>);
       if (ev)
-        hipExtLaunchKernelGGL(k0, g0, dim3(256), 0, s, ev[0], ev[1], 0, a);
+        hipExtLaunchKernelGGL(k0, g0, dim3(GU_THREADS), 0, s, ev[0], ev[1], 0, a);
       else
-        hipLaunchKernelGGL(k0, g0, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(k0, g0, dim3(GU_THREADS), 0, s, a);
       const int st = check_launch("decode_gateup_rows_kernel");
       if (st) return st;
       continue;
