@@ -1593,7 +1593,7 @@ __global__ void __launch_bounds__(kCombineThreads) decode_combine_kernel(LayerAr
 
 // ---- few tokens: the down projection by output rows ------------------------
 // For a few tokens (T * (k + shared) <= ROWS_MAX_SLOTS) a work-group owns
-// ROWS_R output rows across all of the batch's routed slots and sums each
+// rows_r(NCH) output rows across all of the batch's routed slots and sums each
 // token's slots itself: no fp32 partial rows, no counters, no combine tail
 // (at T = 1 that tail is most of the down kernel's time).  A slot's weights
 // are read per slot, so an expert routed by several tokens is read again (from
@@ -1608,7 +1608,12 @@ __global__ void __launch_bounds__(kCombineThreads) decode_combine_kernel(LayerAr
 // lane sums are folded in a fixed order (DPP inside 16-lane rows, then the
 // two rows), and each token's weighted slot rows are summed in ascending slot
 // order: the result does not depend on scheduling.
-constexpr int ROWS_R = 4;        // output rows per work-group
+// Output rows per work-group: 4, or 2 when each lane holds two or more
+// 32-k chunks of a row (I > 1024), which keeps a lane's loads few and the
+// grid twice as wide (DeepSeek-V2-Lite-shaped layer, I = 1408: T=1 17.8 ->
+// 17.1 us per layer, T=2 26.0 -> 24.4; at I <= 1024 two rows were 0.3 us
+// slower).
+constexpr int rows_r(int nch) { return nch >= 2 ? 2 : 4; }
 constexpr int ROWS_MAX_SLOTS = 64;  // T * (k + shared)
 
 template <int CTRL>
@@ -1740,7 +1745,7 @@ __global__ void __launch_bounds__(GU_THREADS) decode_gateup_rows_kernel(LayerArg
 // per lane (all of a lane's loads are issued before its arithmetic).
 template <bool BF, bool MIXED, int NCH, bool ONCE>  // ONCE: one token, each weight row read once
 __global__ void __launch_bounds__(256) decode_down_rows_kernel(LayerArgs a) {
-  constexpr int R = ROWS_R;
+  constexpr int R = rows_r(NCH);
   __shared__ float red[ROWS_MAX_SLOTS][R];
   const int h0 = blockIdx.x * R;
   const int lane = threadIdx.x & 63, hw = threadIdx.x >> 5, l = threadIdx.x & 31;
@@ -2070,7 +2075,7 @@ int launch_decode_layer(const DecodeLaunch& d, hipStream_t s) {
     }
     if (ph == 1 && rows) {
       // few tokens: the down projection by output rows, summed in-kernel
-      const dim3 g1((unsigned)(d.H / ROWS_R));
+      const dim3 g1((unsigned)(d.H / rows_r((d.I / 32 + 31) / 32)));
       const int nch = (d.I / 32 + 31) / 32;  // chunks per lane
       const decode_kernel_t k1 =
           mixed ? (d.bf ? pick_down_rows<true, true>(nch, d.T == 1) : pick_down_rows<false, true>(nch, d.T == 1))
